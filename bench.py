@@ -1,0 +1,184 @@
+"""Depth-render benchmark: G rays/s and ms per batch of the MI355X renderer.
+
+One step = one render of the whole batch (N envs x 128x64 rays) from poses
+already resident in HBM into a preallocated output, on the current stream.
+Default workload: ``ramp_field`` — 2048 envs x 128x64 = 16,777,216 rays over
+a 256x256x128 fp32 grid at 16 u (64 ramps + 16 boxes), max 96 steps,
+hit_eps 1 u, range 6144 u, near 2000 u.
+
+Prints ONE JSON line. ``roofline`` prices the march kernel against HBM:
+algorithmic bytes per launch = sum over rays of (grid loads x voxel bytes)
++ rays x output bytes + envs x 24 B of pose input; the per-ray load counts
+come from the kernel's census mode (run once, outside the timed region), and
+the launch duration from HIP events around the timed launches on the stream
+the kernel runs on. ``cpu_baseline`` times the lockstep torch restatement of
+the reference's CPU render on this host's cores, on a bounded sample of the
+same workload.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+for p in (str(ROOT), str(ROOT / "rl_cs1.6_surf_amd")):
+    if p not in sys.path:
+        sys.path.insert(0, p)
+
+HBM_PEAK_GBS = 8000.0
+METRIC = "G rays/s and ms/batch at 2048 envs×128×64; % of HBM/cache BW roofline"
+
+
+def _log(msg):
+    print(msg, file=sys.stderr, flush=True)
+
+
+def cpu_baseline(w, sc, envs, repeats=3):
+    """Lockstep torch render (the reference's CPU path shape) on host cores."""
+    import torch
+    from oracle import lockstep
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    ps = w.poses(sc, envs)
+    kw = dict(width=w.width, height=w.height, range_units=w.range_units,
+              near_range=w.near_range, hit_eps=w.hit_eps, max_steps=w.max_steps)
+    times = []
+    for _ in range(repeats):
+        t0 = time.perf_counter()
+        lockstep.render(sc.sdf, sc.mins, sc.cell, ps.origin, ps.yaw, ps.pitch, ps.ducked, **kw)
+        times.append(time.perf_counter() - t0)
+    t = statistics.median(times)
+    rays = envs * w.width * w.height
+    model = ""
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return {"value": round(rays / t / 1e9, 6), "unit": "G rays/s", "cores": cores,
+            "kind": "port",
+            "sample": f"{envs} of {w.n_envs} envs of {w.name} ({rays} rays), torch lockstep, "
+                      f"median of {repeats}: {t * 1e3:.1f} ms; cpu: {model}"}
+
+
+def main(argv=None):
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--workload", default="ramp_field")
+    ap.add_argument("--layout", default="brick4", choices=["brick4", "linear"])
+    ap.add_argument("--cpu-envs", type=int, default=512)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    args = ap.parse_args(argv)
+
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        sys.exit("bench.py measures one GPU: the render is per-env data parallel with no "
+                 "exchange, and this build runs on a single MI355X (use --gpus 1)")
+
+    import numpy as np
+    import torch
+    from surfgym import synth, vision
+
+    w = synth.WORKLOADS[args.workload]
+    dev = torch.device("cuda:0")
+    t0 = time.perf_counter()
+    sc = w.scene()
+    ps = w.poses(sc)
+    _log(f"[bench] {w.name}: grid {sc.nz}x{sc.ny}x{sc.nx} baked, {len(ps)} poses "
+         f"({time.perf_counter() - t0:.1f} s)")
+    gdt = torch.float16 if w.store == "f16" else torch.float32
+    odt = torch.bfloat16 if w.out_dtype == "bf16" else torch.float32
+    lid = vision.GpuLidar.from_grid(sc.sdf, sc.mins, sc.cell, width=w.width, height=w.height,
+                                    range_units=w.range_units, near_range=w.near_range,
+                                    max_steps=w.max_steps, hit_eps=w.hit_eps, grid_dtype=gdt,
+                                    layout=args.layout, device=dev)
+    origin = torch.as_tensor(ps.origin, device=dev)
+    yaw = torch.as_tensor(ps.yaw, device=dev)
+    pitch = torch.as_tensor(ps.pitch, device=dev)
+    duck = torch.as_tensor(ps.ducked, device=dev)
+    n = len(ps)
+    out = torch.empty(n, w.height, w.width, dtype=odt, device=dev)
+
+    # census (untimed): grid loads per ray -> algorithmic bytes
+    taps = torch.empty(n, w.height, w.width, dtype=torch.int32, device=dev)
+    lid.render(origin, yaw, pitch, duck, out=out, taps=taps)
+    torch.cuda.synchronize()
+    loads = int(taps.sum(dtype=torch.int64).item())
+    tap_stats = taps.float()
+    rays = n * w.width * w.height
+    vox_b = 2 if w.store == "f16" else 4
+    out_b = 2 if w.out_dtype == "bf16" else 4
+    alg_bytes = loads * vox_b + rays * out_b + n * 24
+    _log(f"[bench] census: {loads} loads, mean {loads / rays:.2f}/ray, "
+         f"max {int(tap_stats.max().item())}")
+    del taps, tap_stats
+
+    stream = torch.cuda.current_stream(dev)
+    for _ in range(args.warmup):
+        lid.render(origin, yaw, pitch, duck, out=out)
+    torch.cuda.synchronize()
+    ev0 = torch.cuda.Event(enable_timing=True)
+    ev1 = torch.cuda.Event(enable_timing=True)
+    per = []
+    t_start = time.perf_counter()
+    ev0.record(stream)
+    for _ in range(args.steps):
+        e_a = torch.cuda.Event(enable_timing=True)
+        e_b = torch.cuda.Event(enable_timing=True)
+        e_a.record(stream)
+        lid.render(origin, yaw, pitch, duck, out=out)
+        e_b.record(stream)
+        per.append((e_a, e_b))
+    ev1.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t_start
+    total_ms = ev0.elapsed_time(ev1)
+    launch_ms = [a.elapsed_time(b) for a, b in per]
+    ms_per_step = total_ms / args.steps
+    avg_launch_ms = sum(launch_ms) / len(launch_ms)
+    med_launch_ms = statistics.median(launch_ms)
+    achieved = alg_bytes / (avg_launch_ms * 1e-3) / 1e9
+    _log(f"[bench] {args.steps} steps: {ms_per_step:.4f} ms/step (events), wall {wall:.3f} s, "
+         f"launch avg {avg_launch_ms:.4f} ms, median {med_launch_ms:.4f} ms")
+
+    res = {
+        "metric": METRIC,
+        "value": round(rays / (ms_per_step * 1e-3) / 1e9, 4),
+        "unit": "G rays/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic",
+        "config": {"workload": w.name, "envs": n, "image": f"{w.width}x{w.height}",
+                   "rays": rays, "grid": f"{sc.nx}x{sc.ny}x{sc.nz} {w.store} @{sc.cell:g}u",
+                   "layout": args.layout, "out": w.out_dtype, "max_steps": w.max_steps,
+                   "hit_eps": w.hit_eps, "range": round(w.range_units, 3),
+                   "near": round(w.near_range, 3), "grid_loads_per_ray": round(loads / rays, 4),
+                   "launch_ms_median": round(med_launch_ms, 5)},
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 5), "traffic": None,
+                     "alg_bytes_per_launch": alg_bytes},
+        "cpu_baseline": None,
+    }
+    if not args.no_cpu:
+        envs = min(args.cpu_envs, n)
+        _log(f"[bench] cpu baseline on {envs} envs ...")
+        res["cpu_baseline"] = cpu_baseline(w, sc, envs)
+    print(json.dumps(res), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,164 @@
+/* sdfr.h — C ABI of the MI355X SDF depth renderer (libsdfr.so).
+ *
+ * Replaces the per-tick render of the reference's GPU lidar,
+ * python/surfgym/vision.py (GpuLidar.__init__ :457-529, GpuLidar.render
+ * :542-550, _render_triton :552-594, _march_kernel :59-116). The reference has
+ * no C ABI for this path: its Python class launches a Triton JIT kernel. This
+ * header is the boundary a ctypes binding (python/surfgym/core.py style:
+ * explicit argtypes, ABI-version refusal) loads instead.
+ *
+ * Conventions follow the reference's own C ABI, src/surfcore.h:
+ *   - every array is caller-allocated; device arrays are plain device pointers
+ *     (e.g. torch tensor data_ptr()), host structs are passed by pointer;
+ *   - creation returns NULL and writes a message into err/errlen
+ *     (surfcore.h:156-157); calls return int32 0 = ok, < 0 = error
+ *     (surfcore.h:162-168) and sdfr_last_error() says why;
+ *   - sdfr_abi_version() is checked by the binding before any other call
+ *     (surfcore.h:61-64, core.py:444-448);
+ *   - one caller at a time per handle (surfcore.h:4-5).
+ *
+ * Work is enqueued on the caller's HIP stream (hipStream_t passed as void*,
+ * NULL = legacy default stream) and never synchronises the host, so renders
+ * order with the caller's other work and can be captured into a hipGraph.
+ */
+#ifndef SDFR_H
+#define SDFR_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define SDFR_API __attribute__((visibility("default")))
+
+/* Bumped on every struct or semantic change; the binding refuses a library
+ * reporting another value. */
+#define SDFR_ABI_VERSION 1
+
+/* Element types of caller arrays. */
+enum {
+    SDFR_F32 = 0,
+    SDFR_F16 = 1,
+    SDFR_BF16 = 2,
+    SDFR_I32 = 3,
+    SDFR_I64 = 4,
+    SDFR_U8 = 5,   /* also torch.bool */
+    SDFR_F64 = 6
+};
+
+/* Device layout of the handle's private copy of the grid. */
+enum {
+    SDFR_LAYOUT_LINEAR = 0, /* [nz][ny][nx], the reference's sdf_flat order (vision.py:476-480) */
+    SDFR_LAYOUT_BRICK4 = 1  /* 4x4x4-voxel bricks, brick-linear, x-fastest inside a brick */
+};
+
+/* Camera models (GpuLidar(pinhole=...), vision.py:484-529). */
+enum {
+    SDFR_CAM_EQUIANGULAR = 0, /* yoff/poff angles added to yaw/pitch (vision.py:502-509) */
+    SDFR_CAM_PINHOLE = 1      /* tangent-plane grid, normalised (vision.py:510-529) */
+};
+
+/* Grid geometry: the reference's single grid definition, grid_dims()
+ * (vision.py:310-322). Voxel (ix,iy,iz) is sampled at mins + (i+0.5)*cell
+ * (env.c:680-682). Values are unsigned distances in map units, 0 in solid. */
+typedef struct SdfrGridDesc {
+    int32_t nx, ny, nz;
+    float mins[3];
+    float cell;
+} SdfrGridDesc;
+
+/* One sensor configuration: the GpuLidar constructor arguments that reach
+ * the march (vision.py:457-509, 99-116). hit_eps and min_step are explicit so
+ * callers can pass the reference's 0.6*cell and 0.3*cell (vision.py:87-88) or
+ * another epsilon. near == range reproduces the legacy t/range encoding. */
+typedef struct SdfrCam {
+    int32_t width, height;  /* W, H: pixels per image row / column */
+    double hfov_deg;        /* equiangular: horizontal field of view (120) */
+    double vfov_deg;        /* equiangular: vertical field of view (90) */
+    double tan_half_h;      /* pinhole: tan(hfov/2) as the host computes it (vision.py:517) */
+    double tan_half_v;      /* pinhole: tan(vfov/2) (vision.py:518) */
+    float range;            /* trace range and clamp (range_units) */
+    float near;             /* linear part of the encoding (near_range) */
+    float hit_eps;          /* stop when the sampled distance <= hit_eps */
+    float min_step;         /* smallest step, max(0.9*d, min_step) */
+    int32_t max_steps;      /* loop trip bound */
+    int32_t camera;         /* SDFR_CAM_* */
+} SdfrCam;
+
+/* Per-env pose inputs (the render() arguments, vision.py:542-550) and the
+ * output image. All pointers are device pointers; strides are in elements
+ * so strided torch views (the trainer passes columns of an (N,6) tensor,
+ * train_fast.py:1757) need no copy. */
+typedef struct SdfrPoses {
+    const float* origin;     /* (N,3) f32, element (n,a) at origin[n*origin_stride + a] */
+    int64_t origin_stride;
+    const float* yaw_deg;    /* (N,) f32 degrees */
+    int64_t yaw_stride;
+    const float* pitch_deg;  /* (N,) f32 degrees */
+    int64_t pitch_stride;
+    const void* ducked;      /* (N,) any SDFR_* numeric type, nonzero = ducked */
+    int64_t ducked_stride;
+    int32_t ducked_dtype;
+    int32_t n_envs;          /* N >= 1 */
+} SdfrPoses;
+
+typedef struct SdfrImage {
+    void* out;               /* depth image, env n row-major HxW at out + n*env_stride elements */
+    int64_t env_stride;      /* elements between envs (H*W for a dense (N,H,W) tensor) */
+    int32_t dtype;           /* SDFR_F32 or SDFR_BF16 */
+    int32_t reserved;
+    int32_t* taps;           /* optional per-ray census, NULL = off: grid loads issued for the ray,
+                                dense (N,H,W) int32 (tools/bench_lidar.py:45-88 counts the same loop) */
+} SdfrImage;
+
+typedef struct SdfrGrid SdfrGrid;
+
+SDFR_API int32_t sdfr_abi_version(void);
+
+/* Builds the handle's device copy of a grid. `src` holds nz*ny*nx values of
+ * `src_dtype` (SDFR_F32 or SDFR_F16) in [nz][ny][nx] order; src_on_device
+ * says whether it is a device pointer (a torch tensor) or host memory.
+ * `store_dtype` (SDFR_F32 or SDFR_F16; the reference stores f16,
+ * vision.py:476-477, rounding to nearest even) and `layout` (SDFR_LAYOUT_*)
+ * pick the device copy. Replaces the grid upload of GpuLidar.__init__
+ * (vision.py:473-480). The copy is complete when the stream reaches it;
+ * the source may be freed after that. NULL + message in err on failure. */
+SDFR_API SdfrGrid* sdfr_grid_create(const SdfrGridDesc* desc, const void* src,
+                                    int32_t src_dtype, int32_t src_on_device,
+                                    int32_t store_dtype, int32_t layout,
+                                    void* stream, char* err, int32_t errlen);
+
+SDFR_API void sdfr_grid_destroy(SdfrGrid* grid);
+
+/* Bytes of device memory the handle owns (the re-laid-out grid). */
+SDFR_API int64_t sdfr_grid_bytes(const SdfrGrid* grid);
+
+/* Renders N depth images: equiangular (or pinhole) rays from each env's eye,
+ * nearest-neighbour sphere trace through the grid, near-linear/far-compressed
+ * encoding. Replaces GpuLidar._render_triton + _march_kernel
+ * (vision.py:552-594, 59-116); results are per-ray and independent of N and
+ * of how rays are scheduled. Asynchronous on `stream`; allocates nothing.
+ * Returns 0, or < 0 with sdfr_last_error() set (bad handle/argument, launch
+ * failure). */
+SDFR_API int32_t sdfr_render(const SdfrGrid* grid, const SdfrCam* cam,
+                             const SdfrPoses* poses, const SdfrImage* image,
+                             void* stream);
+
+/* Writes the unit direction of every ray, dirs[n][r][c][0..2] (dense f32),
+ * with the same code the march uses to cast it; origin and ducked are not
+ * read. The reference exposes the same quantity on its CPU path as
+ * GpuLidar._dirs_equiangular / _dirs_pinhole (vision.py:596-624), which its
+ * camera tests inspect (tests/python/test_pinhole.py:36-41). Asynchronous on
+ * `stream`. */
+SDFR_API int32_t sdfr_ray_dirs(const SdfrCam* cam, const SdfrPoses* poses, float* dirs,
+                               void* stream);
+
+/* Message of the calling thread's most recent error ("" if none). */
+SDFR_API const char* sdfr_last_error(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SDFR_H */

@@ -1,0 +1,155 @@
+"""CPU oracle for the SDF depth render — TEST INFRASTRUCTURE ONLY.
+
+Only tests/, ``__graft_entry__.smoke()`` and bench.py's CPU-baseline leg may
+import this package: it is the checker the GPU renderer is measured against,
+never part of the product path.
+
+Two restatements of the reference's render (python/surfgym/vision.py):
+
+* :func:`render` — per-ray C loop (``oracle/march.c``), the canonical checker.
+  It also returns the number of grid loads each ray issued (the census of
+  tools/bench_lidar.py:45-88), which is the algorithmic-bytes count.
+* :mod:`oracle.lockstep` — the reference's CPU fallback shape
+  (``_render_torch``, vision.py:626-666): torch tensors over all rays in
+  lockstep, with a host ``any()`` check every 8 steps. It is the CPU
+  baseline that bench.py times.
+
+Every function here is pinned by tests/test_oracle.py (closed forms,
+invariants, brute force on tiny inputs) and by the committed fixtures in
+tests/golden/.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+from pathlib import Path
+
+import numpy as np
+
+HERE = Path(__file__).resolve().parent
+LIB_PATH = HERE / "liboracle_march.so"
+
+_lib = None
+
+
+def build(verbose: bool = False) -> Path:
+    """Compile march.c with gcc (IEEE fp32, no contraction, OpenMP)."""
+    import subprocess
+    cmd = ["gcc", "-O2", "-std=c11", "-fPIC", "-shared", "-fopenmp",
+           "-ffp-contract=off", "-fno-fast-math", "-fvisibility=hidden",
+           str(HERE / "march.c"), "-o", str(LIB_PATH) + ".tmp", "-lm"]
+    if verbose:
+        print(" ".join(cmd))
+    subprocess.run(cmd, check=True)
+    os.replace(str(LIB_PATH) + ".tmp", LIB_PATH)
+    return LIB_PATH
+
+
+def _load():
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not LIB_PATH.exists():
+        build()
+    lib = ctypes.CDLL(str(LIB_PATH))
+    f, i, d, p = ctypes.c_float, ctypes.c_int, ctypes.c_double, ctypes.c_void_p
+    lib.oracle_equiangular_offset.restype = f
+    lib.oracle_equiangular_offset.argtypes = [i, i, d]
+    lib.oracle_pinhole_u.restype = f
+    lib.oracle_pinhole_u.argtypes = [i, i, d]
+    lib.oracle_pinhole_v.restype = f
+    lib.oracle_pinhole_v.argtypes = [i, i, d]
+    lib.oracle_ray_dir.restype = None
+    lib.oracle_ray_dir.argtypes = [i, i, i, i, i, d, d, d, d, f, f, p]
+    lib.oracle_encode.restype = f
+    lib.oracle_encode.argtypes = [f, f]
+    lib.oracle_march_ray.restype = f
+    lib.oracle_march_ray.argtypes = [p, i, i, i, p, f, f, f, f, f, f, f, f, f, f, i, p]
+    lib.oracle_render.restype = i
+    lib.oracle_render.argtypes = [p, i, i, i, p, f, i, i, i, d, d, d, d, f, f, f, f, i,
+                                  p, p, p, p, i, p, p, i]
+    _lib = lib
+    return lib
+
+
+def _ptr(a: np.ndarray):
+    return a.ctypes.data_as(ctypes.c_void_p)
+
+
+def as_stored(grid: np.ndarray, store: str) -> np.ndarray:
+    """The voxel values the renderer reads: f32 as given, or rounded to f16
+    (round to nearest even, as torch's ``.to(torch.float16)``, vision.py:476)
+    and widened back."""
+    g = np.ascontiguousarray(grid, dtype=np.float32)
+    if store in ("f16", "float16"):
+        return g.astype(np.float16).astype(np.float32)
+    if store in ("f32", "float32"):
+        return g
+    raise ValueError(f"unknown store dtype {store!r}")
+
+
+def render(grid, mins, cell, origin, yaw_deg, pitch_deg, ducked, *, width=128, height=64,
+           hfov_deg=120.0, vfov_deg=90.0, range_units=2000.0, near_range=None,
+           hit_eps=None, min_step=None, max_steps=64, pinhole=False, store="f32",
+           threads=0):
+    """Depth encodings (N,H,W) f32 and grid loads per ray (N,H,W) int32.
+
+    Defaults and derived constants follow GpuLidar (vision.py:457-509):
+    near = range when not given, hit_eps = 0.6*cell, min_step = 0.3*cell
+    (vision.py:87-88, 637-638), both rounded to fp32 as the comparison does.
+    """
+    lib = _load()
+    g = as_stored(grid, store)
+    nz, ny, nx = g.shape
+    mins = np.ascontiguousarray(mins, dtype=np.float32).reshape(3)
+    origin = np.ascontiguousarray(origin, dtype=np.float32).reshape(-1, 3)
+    n = origin.shape[0]
+    yaw = np.ascontiguousarray(yaw_deg, dtype=np.float32).reshape(n)
+    pitch = np.ascontiguousarray(pitch_deg, dtype=np.float32).reshape(n)
+    duck = np.ascontiguousarray(np.asarray(ducked, dtype=np.float64) != 0, dtype=np.float32).reshape(n)
+    rng = float(range_units)
+    near = float(near_range) if near_range else rng
+    eps = float(np.float32(0.6 * cell)) if hit_eps is None else float(hit_eps)
+    mstep = float(np.float32(0.3 * cell)) if min_step is None else float(min_step)
+    tan_h = float(np.tan(0.5 * hfov_deg * (np.pi / 180.0)))
+    tan_v = float(np.tan(0.5 * vfov_deg * (np.pi / 180.0)))
+    out = np.empty((n, height, width), np.float32)
+    loads = np.empty((n, height, width), np.int32)
+    rc = lib.oracle_render(_ptr(g), nx, ny, nz, _ptr(mins), float(cell), width, height,
+                           1 if pinhole else 0, float(hfov_deg), float(vfov_deg), tan_h, tan_v,
+                           rng, near, eps, mstep, int(max_steps), _ptr(origin), _ptr(yaw),
+                           _ptr(pitch), _ptr(duck), n, _ptr(out), _ptr(loads), int(threads))
+    if rc != 0:
+        raise ValueError("oracle_render rejected its arguments")
+    return out, loads
+
+
+def ray_dirs(width, height, yaw_deg, pitch_deg, *, hfov_deg=120.0, vfov_deg=90.0,
+             pinhole=False):
+    """(H,W,3) unit ray directions of one pose, as the oracle's march uses."""
+    lib = _load()
+    tan_h = float(np.tan(0.5 * hfov_deg * (np.pi / 180.0)))
+    tan_v = float(np.tan(0.5 * vfov_deg * (np.pi / 180.0)))
+    out = np.empty((height, width, 3), np.float32)
+    buf = np.empty(3, np.float32)
+    for r in range(height):
+        for c in range(width):
+            lib.oracle_ray_dir(1 if pinhole else 0, r, c, width, height, float(hfov_deg),
+                               float(vfov_deg), tan_h, tan_v, float(yaw_deg),
+                               float(pitch_deg), _ptr(buf))
+            out[r, c] = buf
+    return out
+
+
+def encode(t: float, near: float) -> float:
+    return float(_load().oracle_encode(float(t), float(near)))
+
+
+def offsets(width, height, hfov_deg=120.0, vfov_deg=90.0):
+    """The equiangular (yoff (W,), poff (H,)) tables as f32."""
+    lib = _load()
+    yo = np.array([lib.oracle_equiangular_offset(c, width, float(hfov_deg))
+                   for c in range(width)], np.float32)
+    po = np.array([lib.oracle_equiangular_offset(r, height, float(vfov_deg))
+                   for r in range(height)], np.float32)
+    return yo, po

@@ -1,0 +1,321 @@
+"""GPU lidar: batched depth images by sphere tracing a voxel SDF on MI355X.
+
+Drop-in for the reference's ``surfgym.vision`` render path
+(python/surfgym/vision.py): ``GpuLidar`` keeps the constructor, ``render``
+signature and output contract (vision.py:457-462, :542-550), and
+``grid_dims``/``pick_cell``/``build_sdf`` keep their meaning, so the
+trainer's rollout loop (train_fast.py:1744-1765) calls it unchanged. The
+render runs in libsdfr.so (hand-written HIP for gfx950, include/sdfr.h),
+enqueued on the current torch stream with no host synchronisation.
+
+Camera convention (src/surfcore.h:20-34): row 0 looks up (+vfov/2), column 0
+looks left (+hfov/2), positive pitch is up, eye height 17 standing / 12
+ducked. Output values: near-linear ``min(t,near)/near`` plus a bounded far
+tail ``0.25*(1-exp(-(t-near)/2500))``; near == range is the legacy
+``t/range`` clamped to 1 (vision.py:112-116, :468-472).
+
+There is deliberately no CPU render: ``device`` must be a ROCm GPU, and a
+missing native library is an error, not a fallback.
+"""
+from __future__ import annotations
+
+import ctypes
+from pathlib import Path
+
+import numpy as np
+import torch
+
+from . import _sdfr
+
+__all__ = ["GpuLidar", "build_sdf", "pick_cell", "grid_dims", "SOLID_ENT_CLASSES"]
+
+# brush entities the reference's physics collides with (vision.py:301-307);
+# kept for importers of the name, the bake itself is not part of this module
+SOLID_ENT_CLASSES = {"func_wall", "func_breakable", "func_pushable",
+                     "func_button", "func_train", "func_conveyor",
+                     "func_wall_toggle", "func_rotating",
+                     "func_door_rotating", "func_door"}
+
+_SDF_BUILDER_VERSION = 2
+_SDF_SEMANTICS = "s4"
+
+_DUCK_DTYPES = {torch.float32: _sdfr.F32, torch.float16: _sdfr.F16, torch.bfloat16: _sdfr.BF16,
+                torch.int32: _sdfr.I32, torch.int64: _sdfr.I64, torch.uint8: _sdfr.U8,
+                torch.bool: _sdfr.U8, torch.float64: _sdfr.F64}
+_GRID_DTYPES = {torch.float32: _sdfr.F32, torch.float16: _sdfr.F16}
+_OUT_DTYPES = {torch.float32: _sdfr.F32, torch.bfloat16: _sdfr.BF16}
+_LAYOUTS = {"linear": _sdfr.LAYOUT_LINEAR, "brick4": _sdfr.LAYOUT_BRICK4}
+
+
+def pick_cell(core, budget_voxels: float = 700e6) -> float:
+    """Smallest power-of-two voxel size from 16 u whose padded grid fits the
+    voxel budget (the reference's rule, vision.py:283-298)."""
+    mn, mx = (np.asarray(v, np.float64) for v in core.map_bounds())
+    cell = 16.0
+    while cell < 256.0:
+        ext = (mx - mn) + 2.0 * (4.0 * cell)
+        if float(np.prod(np.ceil(ext / cell))) <= budget_voxels:
+            break
+        cell *= 2.0
+    return cell
+
+
+def grid_dims(core, cell: float):
+    """(mins float64 (3,), nx, ny, nz): the map bounds padded by 4 cells and
+    cut into whole voxels (vision.py:310-322)."""
+    mn, mx = (np.asarray(v, np.float64) for v in core.map_bounds())
+    pad = 4.0 * cell
+    mins = mn - pad
+    nx, ny, nz = (int(np.ceil(e / cell)) for e in (mx + pad) - mins)
+    return mins, nx, ny, nz
+
+
+def build_sdf(core, cell: float = 16.0, cache_dir=None):
+    """Load the map's baked distance field: (sdf [nz,ny,nx], mins (3,), cell).
+
+    Reads the reference's cache file ``<map>.sdf_<cell>.npz`` (keys sdf, mins,
+    cell, sig) and honours its signature (vision.py:268-280, :420-426), so an
+    existing bake is used as-is. Baking a map from scratch (BSP occupancy
+    sampling through the C core plus an EDT, vision.py:428-438) is not part of
+    this renderer; construct with :meth:`GpuLidar.from_grid` for any other
+    grid. Tests replace this function on the module, as the reference's do.
+    """
+    bsp = Path(core.bsp_path)
+    st = bsp.stat()
+    sig = f"v{_SDF_BUILDER_VERSION}_{st.st_size}_{st.st_mtime_ns}_{_SDF_SEMANTICS}"
+    cache = Path(cache_dir) if cache_dir else bsp.parent
+    f = cache / f"{bsp.stem}.sdf_{cell:g}.npz"
+    if f.exists():
+        z = np.load(f, allow_pickle=False)
+        if "sig" in z and str(z["sig"]) == sig:
+            return z["sdf"], z["mins"], float(z["cell"])
+    raise FileNotFoundError(
+        f"no current SDF bake at {f} (signature {sig}); bake it once with the "
+        "reference's build_sdf, or pass a grid to GpuLidar.from_grid")
+
+
+def _ducked_code(t: torch.Tensor) -> int:
+    return _DUCK_DTYPES.get(t.dtype, -1)
+
+
+class GpuLidar:
+    """Batched depth-image renderer over a voxel SDF.
+
+    ``render(origin, yaw_deg, pitch_deg, ducked) -> (N, H, W) float32`` on
+    the lidar's device; values = hit distance / range, 1.0 = clear (plus the
+    far tail when ``near_range`` < range).
+
+    Keyword-only extensions (defaults reproduce the reference):
+
+    * ``grid_dtype`` — voxel storage, torch.float16 as the reference stores
+      it (vision.py:476-477) or torch.float32;
+    * ``layout`` — the device copy's order, "brick4" (4x4x4 bricks) or
+      "linear";
+    * ``hit_eps`` / ``min_step`` — the step rule's constants, 0.6*cell and
+      0.3*cell by default (vision.py:87-88).
+    """
+
+    def __init__(self, core, width: int = 128, height: int = 64,
+                 hfov_deg: float = 120.0, vfov_deg: float = 90.0,
+                 range_units: float = 2000.0, cell: float = 16.0,
+                 max_steps: int = 64, near_range: float = None,
+                 device="cuda", surf_mask: bool = False,
+                 pinhole: bool = False, *, grid_dtype=torch.float16,
+                 layout: str = "brick4", hit_eps: float = None,
+                 min_step: float = None, _grid=None) -> None:
+        if surf_mask and pinhole:
+            raise ValueError(
+                "surf_mask and pinhole are separate experiments and there is "
+                "no combined kernel")
+        if surf_mask:
+            raise NotImplementedError("the |n_z| surf-mask channel is not built in this renderer")
+        self.device = torch.device(device)
+        if self.device.type != "cuda":
+            raise ValueError(f"GpuLidar renders on a ROCm GPU (device='cuda'), got {device!r}; "
+                             "this renderer has no CPU path")
+        if self.device.index is None:
+            self.device = torch.device("cuda", torch.cuda.current_device())
+        if grid_dtype not in _GRID_DTYPES:
+            raise ValueError(f"grid_dtype must be torch.float16 or torch.float32, got {grid_dtype}")
+        if layout not in _LAYOUTS:
+            raise ValueError(f"layout must be one of {sorted(_LAYOUTS)}, got {layout!r}")
+        self._lib = _sdfr.load()
+        sdf, mins, cell = _grid if _grid is not None else build_sdf(core, cell)
+        sdf = np.asarray(sdf)
+        if sdf.ndim != 3:
+            raise ValueError(f"the grid must be [nz, ny, nx], got shape {sdf.shape}")
+        # flat grid + integer strides, the reference's attributes (vision.py:476-480)
+        self.sdf_flat = torch.as_tensor(sdf, device=self.device).to(grid_dtype).reshape(-1)
+        self.nz, self.ny, self.nx = (int(v) for v in sdf.shape)
+        self.stride_z = self.ny * self.nx
+        self.stride_y = self.nx
+        mins = np.asarray(mins, np.float32).reshape(3)
+        self.mins = torch.as_tensor(mins, device=self.device)
+        self.mins_f = (float(mins[0]), float(mins[1]), float(mins[2]))
+        self.cell = float(cell)
+        self.surf_mask = False
+        self.channels = 1
+        self.W, self.H = int(width), int(height)
+        self.range = float(range_units)
+        self.near = float(near_range) if near_range else self.range
+        self.max_steps = int(max_steps)
+        self.hfov_deg, self.vfov_deg = float(hfov_deg), float(vfov_deg)
+        # the march compares in fp32 (vision.py:87-88, 637-638)
+        self.hit_eps = float(np.float32(0.6 * self.cell if hit_eps is None else hit_eps))
+        self.min_step = float(np.float32(0.3 * self.cell if min_step is None else min_step))
+        d2r = np.pi / 180.0
+        # per-pixel angular offsets (surfcore.h convention); the kernel derives
+        # the same float64-then-fp32 values in registers, these are for callers
+        yoff = (self.hfov_deg * (0.5 - (np.arange(self.W) + 0.5) / self.W)) * d2r
+        poff = (self.vfov_deg * (0.5 - (np.arange(self.H) + 0.5) / self.H)) * d2r
+        self.yoff = torch.as_tensor(yoff, dtype=torch.float32, device=self.device)
+        self.poff = torch.as_tensor(poff, dtype=torch.float32, device=self.device)
+        self.pinhole = bool(pinhole)
+        self._tan_h = float(np.tan(0.5 * self.hfov_deg * d2r))
+        self._tan_v = float(np.tan(0.5 * self.vfov_deg * d2r))
+        if self.pinhole:
+            uo = self._tan_h * (2.0 * np.arange(self.W) / max(self.W - 1, 1) - 1.0)
+            vo = self._tan_v * (1.0 - 2.0 * np.arange(self.H) / max(self.H - 1, 1))
+            if self.W == 1:
+                uo[:] = 0.0
+            if self.H == 1:
+                vo[:] = 0.0
+            self.uoff = torch.as_tensor(uo, dtype=torch.float32, device=self.device)
+            self.voff = torch.as_tensor(vo, dtype=torch.float32, device=self.device)
+        self.layout = layout
+        self.grid_dtype = grid_dtype
+        desc = _sdfr.GridDesc(self.nx, self.ny, self.nz, (ctypes.c_float * 3)(*mins),
+                              self.cell)
+        err = ctypes.create_string_buffer(512)
+        with torch.cuda.device(self.device):
+            stream = torch.cuda.current_stream(self.device)
+            h = self._lib.sdfr_grid_create(ctypes.byref(desc), self.sdf_flat.data_ptr(),
+                                           _GRID_DTYPES[grid_dtype], 1, _GRID_DTYPES[grid_dtype],
+                                           _LAYOUTS[layout], stream.cuda_stream, err, len(err))
+        if not h:
+            raise _sdfr.SdfrError(err.value.decode("utf-8", "replace"))
+        self._grid = h
+
+    @classmethod
+    def from_grid(cls, sdf, mins, cell, **kwargs) -> "GpuLidar":
+        """A lidar over an explicit [nz,ny,nx] distance grid (no map core)."""
+        kwargs = dict(kwargs)
+        kwargs["cell"] = float(cell)
+        return cls(None, _grid=(sdf, mins, float(cell)), **kwargs)
+
+    def __del__(self):
+        h = getattr(self, "_grid", None)
+        if h:
+            self._grid = None
+            try:
+                torch.cuda.synchronize(self.device)
+            except Exception:
+                pass
+            self._lib.sdfr_grid_destroy(h)
+
+    # ------------------------------------------------------------------ args --
+    def _cam(self) -> _sdfr.Cam:
+        return _sdfr.Cam(self.W, self.H, self.hfov_deg, self.vfov_deg, self._tan_h, self._tan_v,
+                         self.range, self.near, self.hit_eps, self.min_step, self.max_steps,
+                         _sdfr.CAM_PINHOLE if self.pinhole else _sdfr.CAM_EQUIANGULAR)
+
+    def _f32(self, t, name):
+        t = torch.as_tensor(t)
+        if t.device != self.device or t.dtype != torch.float32:
+            t = t.to(self.device, torch.float32)
+        return t
+
+    def _poses(self, origin, yaw_deg, pitch_deg, ducked):
+        origin = self._f32(origin, "origin")
+        if origin.dim() != 2 or origin.shape[1] != 3:
+            raise ValueError(f"origin must be (N, 3), got {tuple(origin.shape)}")
+        if origin.stride(1) != 1:
+            origin = origin.contiguous()
+        n = origin.shape[0]
+        if n < 1:
+            raise ValueError("render needs at least one env")
+        yaw = self._f32(yaw_deg, "yaw_deg").reshape(-1)
+        pitch = self._f32(pitch_deg, "pitch_deg").reshape(-1)
+        ducked = torch.as_tensor(ducked)
+        if ducked.device != self.device:
+            ducked = ducked.to(self.device)
+        ducked = ducked.reshape(-1)
+        if _ducked_code(ducked) < 0:
+            ducked = ducked.to(torch.int32)
+        for name, t in (("yaw_deg", yaw), ("pitch_deg", pitch), ("ducked", ducked)):
+            if t.shape[0] != n:
+                raise ValueError(f"{name} has {t.shape[0]} entries for {n} envs")
+        p = _sdfr.Poses(origin.data_ptr(), origin.stride(0), yaw.data_ptr(), yaw.stride(0),
+                        pitch.data_ptr(), pitch.stride(0), ducked.data_ptr(), ducked.stride(0),
+                        _ducked_code(ducked), n)
+        return p, (origin, yaw, pitch, ducked)
+
+    def _check_out(self, out: torch.Tensor, n: int) -> int:
+        if out.device != self.device or out.dtype not in _OUT_DTYPES:
+            raise ValueError("out must be a float32 or bfloat16 tensor on the lidar's device")
+        if out.shape[0] != n or out[0].numel() != self.H * self.W:
+            raise ValueError(f"out must hold N={n} images of {self.H}x{self.W}, "
+                             f"got {tuple(out.shape)}")
+        # each env's image must be one dense row-major HxW block
+        inner = out[0]
+        expect = 1
+        for size, stride in reversed(list(zip(inner.shape, inner.stride()))):
+            if size != 1 and stride != expect:
+                raise ValueError("each env's image in out must be contiguous")
+            expect *= size
+        return out.stride(0) if n > 1 else self.H * self.W
+
+    # ---------------------------------------------------------------- render --
+    @torch.no_grad()
+    def render(self, origin, yaw_deg, pitch_deg, ducked, out=None, taps=None):
+        """origin (N,3), yaw/pitch (N,) degrees, ducked (N,) bool/int/float ->
+        (N, H, W) float32 depth encodings (vision.py:542-550).
+
+        Inputs may be strided views (the trainer passes columns of its (N,6)
+        pose tensor). ``out`` optionally names the destination — any float32
+        or bfloat16 tensor whose dim 0 is N and whose per-env block is a dense
+        HxW image (e.g. the image columns of an observation row); it is
+        returned. ``taps`` optionally receives the grid loads each ray issued
+        ((N,H,W) int32), for measurement."""
+        poses, keep = self._poses(origin, yaw_deg, pitch_deg, ducked)
+        n = poses.n_envs
+        if out is None:
+            out = torch.empty(n, self.H, self.W, device=self.device)
+        env_stride = self._check_out(out, n)
+        taps_ptr = None
+        if taps is not None:
+            if (taps.device != self.device or taps.dtype != torch.int32 or not taps.is_contiguous()
+                    or taps.numel() != n * self.H * self.W):
+                raise ValueError("taps must be a contiguous int32 (N,H,W) tensor on the device")
+            taps_ptr = taps.data_ptr()
+        img = _sdfr.Image(out.data_ptr(), env_stride, _OUT_DTYPES[out.dtype], 0, taps_ptr)
+        with torch.cuda.device(self.device):
+            stream = torch.cuda.current_stream(self.device).cuda_stream
+            rc = self._lib.sdfr_render(self._grid, ctypes.byref(self._cam()), ctypes.byref(poses),
+                                       ctypes.byref(img), stream)
+        _sdfr.check(rc, "sdfr_render", self._lib)
+        del keep
+        return out
+
+    @torch.no_grad()
+    def ray_dirs(self, yaw_deg, pitch_deg) -> torch.Tensor:
+        """(N, H, W, 3) unit ray directions exactly as the march casts them."""
+        yaw = self._f32(yaw_deg, "yaw_deg").reshape(-1)
+        pitch = self._f32(pitch_deg, "pitch_deg").reshape(-1)
+        n = yaw.shape[0]
+        zeros = torch.zeros(n, 3, device=self.device)
+        duck = torch.zeros(n, dtype=torch.int32, device=self.device)
+        poses, keep = self._poses(zeros, yaw, pitch, duck)
+        out = torch.empty(n, self.H, self.W, 3, device=self.device)
+        with torch.cuda.device(self.device):
+            stream = torch.cuda.current_stream(self.device).cuda_stream
+            rc = self._lib.sdfr_ray_dirs(ctypes.byref(self._cam()), ctypes.byref(poses),
+                                         out.data_ptr(), stream)
+        _sdfr.check(rc, "sdfr_ray_dirs", self._lib)
+        del keep
+        return out
+
+    @property
+    def grid_bytes(self) -> int:
+        """Device bytes of the re-laid-out grid the kernel reads."""
+        return int(self._lib.sdfr_grid_bytes(self._grid))
