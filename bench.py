@@ -68,6 +68,30 @@ def cpu_baseline(w, sc, envs, repeats=3):
                       f"median of {repeats}: {t * 1e3:.1f} ms; cpu: {model}"}
 
 
+def copy_bandwidth(dev, n_bytes=2_000_000_000, iters=10):
+    """Device copy bandwidth, 2 x bytes / time (read + write), median of
+    `iters` copies of an n_bytes buffer: the reference's health check method
+    (tools/gpu_health.py:76-78). Also the plain copy kernel whose HBM
+    counters calibrate the march kernel's FETCH_SIZE / WRITE_SIZE."""
+    import torch
+    a = torch.empty(n_bytes // 2, dtype=torch.bfloat16, device=dev)
+    b = torch.empty_like(a)
+    b.copy_(a)
+    torch.cuda.synchronize()
+    ms = []
+    for _ in range(iters):
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record()
+        b.copy_(a)
+        e1.record()
+        torch.cuda.synchronize()
+        ms.append(e0.elapsed_time(e1))
+    del a, b
+    torch.cuda.empty_cache()
+    return 2 * n_bytes / (statistics.median(ms) * 1e-3) / 1e9
+
+
 def main(argv=None):
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -75,8 +99,14 @@ def main(argv=None):
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--workload", default="ramp_field")
     ap.add_argument("--layout", default="brick4", choices=["brick4", "linear"])
+    ap.add_argument("--schedule", default="tiles", choices=["persistent", "tiles"])
+    ap.add_argument("--refill", type=int, default=16, help="free lanes that trigger a refill")
+    ap.add_argument("--rpl", type=int, default=2, help="tiles schedule: rays per lane (1, 2, 4)")
     ap.add_argument("--cpu-envs", type=int, default=512)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--no-copy", action="store_true", help="skip the copy-bandwidth probe")
+    ap.add_argument("--graph", action="store_true",
+                    help="capture one render in a hipGraph and time graph replays")
     args = ap.parse_args(argv)
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -99,7 +129,9 @@ def main(argv=None):
     lid = vision.GpuLidar.from_grid(sc.sdf, sc.mins, sc.cell, width=w.width, height=w.height,
                                     range_units=w.range_units, near_range=w.near_range,
                                     max_steps=w.max_steps, hit_eps=w.hit_eps, grid_dtype=gdt,
-                                    layout=args.layout, device=dev)
+                                    layout=args.layout, schedule=args.schedule,
+                                    refill_lanes=args.refill, rays_per_lane=args.rpl,
+                                    device=dev)
     origin = torch.as_tensor(ps.origin, device=dev)
     yaw = torch.as_tensor(ps.yaw, device=dev)
     pitch = torch.as_tensor(ps.pitch, device=dev)
@@ -121,9 +153,23 @@ def main(argv=None):
          f"max {int(tap_stats.max().item())}")
     del taps, tap_stats
 
+    step = lambda: lid.render(origin, yaw, pitch, duck, out=out)   # noqa: E731
+    if args.graph:
+        # the rollout step's render as a captured graph (capture on a side
+        # stream after an eager warm-up render, then replay on the current one)
+        side = torch.cuda.Stream(device=dev)
+        side.wait_stream(torch.cuda.current_stream(dev))
+        with torch.cuda.stream(side):
+            lid.render(origin, yaw, pitch, duck, out=out)
+        torch.cuda.current_stream(dev).wait_stream(side)
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            lid.render(origin, yaw, pitch, duck, out=out)
+        step = graph.replay
     stream = torch.cuda.current_stream(dev)
     for _ in range(args.warmup):
-        lid.render(origin, yaw, pitch, duck, out=out)
+        step()
     torch.cuda.synchronize()
     ev0 = torch.cuda.Event(enable_timing=True)
     ev1 = torch.cuda.Event(enable_timing=True)
@@ -134,7 +180,7 @@ def main(argv=None):
         e_a = torch.cuda.Event(enable_timing=True)
         e_b = torch.cuda.Event(enable_timing=True)
         e_a.record(stream)
-        lid.render(origin, yaw, pitch, duck, out=out)
+        step()
         e_b.record(stream)
         per.append((e_a, e_b))
     ev1.record(stream)
@@ -149,6 +195,9 @@ def main(argv=None):
     _log(f"[bench] {args.steps} steps: {ms_per_step:.4f} ms/step (events), wall {wall:.3f} s, "
          f"launch avg {avg_launch_ms:.4f} ms, median {med_launch_ms:.4f} ms")
 
+    copy_gbs = None if args.no_copy else copy_bandwidth(dev)
+    if copy_gbs:
+        _log(f"[bench] device copy {copy_gbs:.0f} GB/s")
     res = {
         "metric": METRIC,
         "value": round(rays / (ms_per_step * 1e-3) / 1e9, 4),
@@ -164,13 +213,18 @@ def main(argv=None):
         "data": "synthetic",
         "config": {"workload": w.name, "envs": n, "image": f"{w.width}x{w.height}",
                    "rays": rays, "grid": f"{sc.nx}x{sc.ny}x{sc.nz} {w.store} @{sc.cell:g}u",
-                   "layout": args.layout, "out": w.out_dtype, "max_steps": w.max_steps,
+                   "layout": args.layout, "schedule": args.schedule, "refill_lanes": args.refill,
+                   "rays_per_lane": args.rpl,
+                   "out": w.out_dtype, "max_steps": w.max_steps,
                    "hit_eps": w.hit_eps, "range": round(w.range_units, 3),
                    "near": round(w.near_range, 3), "grid_loads_per_ray": round(loads / rays, 4),
+                   "graph": bool(args.graph),
                    "launch_ms_median": round(med_launch_ms, 5)},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 5), "traffic": None,
-                     "alg_bytes_per_launch": alg_bytes},
+                     "alg_bytes_per_launch": alg_bytes,
+                     "copy_gbs": round(copy_gbs, 1) if copy_gbs else None,
+                     "frac_of_copy": round(achieved / copy_gbs, 5) if copy_gbs else None},
         "cpu_baseline": None,
     }
     if not args.no_cpu:

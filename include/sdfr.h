@@ -34,7 +34,7 @@ extern "C" {
 
 /* Bumped on every struct or semantic change; the binding refuses a library
  * reporting another value. */
-#define SDFR_ABI_VERSION 1
+#define SDFR_ABI_VERSION 2
 
 /* Element types of caller arrays. */
 enum {
@@ -57,6 +57,12 @@ enum {
 enum {
     SDFR_CAM_EQUIANGULAR = 0, /* yoff/poff angles added to yaw/pitch (vision.py:502-509) */
     SDFR_CAM_PINHOLE = 1      /* tangent-plane grid, normalised (vision.py:510-529) */
+};
+
+/* Work schedules of sdfr_render (both give identical results). */
+enum {
+    SDFR_SCHED_PERSISTENT = 0, /* persistent waves refilling ended rays' lanes */
+    SDFR_SCHED_TILES = 1       /* default: launch-scheduled waves of 8x8 pixel tiles */
 };
 
 /* Grid geometry: the reference's single grid definition, grid_dims()
@@ -131,19 +137,35 @@ SDFR_API SdfrGrid* sdfr_grid_create(const SdfrGridDesc* desc, const void* src,
 
 SDFR_API void sdfr_grid_destroy(SdfrGrid* grid);
 
+/* Chooses how sdfr_render schedules rays on this handle: `schedule` is an
+ * SDFR_SCHED_* value (default SDFR_SCHED_TILES); `refill_lanes` (1..64,
+ * default 16) is the number of free lanes at which a persistent wave takes
+ * new rays; `rays_per_lane` (1, 2 or 4, default 2) is how many tiles a wave
+ * of the tiles schedule marches at once. Results do not depend on any of them. No reference
+ * counterpart: the Triton launch has one fixed shape (vision.py:48-54;
+ * tools/proto_march.py sweeps it). */
+SDFR_API int32_t sdfr_grid_set_schedule(SdfrGrid* grid, int32_t schedule, int32_t refill_lanes,
+                                        int32_t rays_per_lane);
+
 /* Bytes of device memory the handle owns (the re-laid-out grid). */
 SDFR_API int64_t sdfr_grid_bytes(const SdfrGrid* grid);
+
+/* Device bytes of the workspace sdfr_render needs for n_envs envs of this
+ * camera: per env (W + H + 4) float2 of ray tables. < 0 on bad arguments. */
+SDFR_API int64_t sdfr_workspace_bytes(const SdfrCam* cam, int32_t n_envs);
 
 /* Renders N depth images: equiangular (or pinhole) rays from each env's eye,
  * nearest-neighbour sphere trace through the grid, near-linear/far-compressed
  * encoding. Replaces GpuLidar._render_triton + _march_kernel
  * (vision.py:552-594, 59-116); results are per-ray and independent of N and
- * of how rays are scheduled. Asynchronous on `stream`; allocates nothing.
- * Returns 0, or < 0 with sdfr_last_error() set (bad handle/argument, launch
- * failure). */
+ * of how rays are scheduled. `workspace` is caller-owned device memory of at
+ * least sdfr_workspace_bytes() bytes, 8-byte aligned; its contents need no
+ * initialisation and are dead after the call. Asynchronous on `stream`;
+ * allocates nothing. Returns 0, or < 0 with sdfr_last_error() set (bad
+ * handle/argument, launch failure). */
 SDFR_API int32_t sdfr_render(const SdfrGrid* grid, const SdfrCam* cam,
                              const SdfrPoses* poses, const SdfrImage* image,
-                             void* stream);
+                             void* workspace, int64_t workspace_size, void* stream);
 
 /* Writes the unit direction of every ray, dirs[n][r][c][0..2] (dense f32),
  * with the same code the march uses to cast it; origin and ducked are not

@@ -23,20 +23,30 @@
 // are evaluated in fp64 and rounded once to fp32, which gives the correctly
 // rounded fp32 value except in cases rarer than 1 in 2^28.
 //
-// Work decomposition. One wave64 owns a 2-D tile of pixels of one env (8x8
-// by default): neighbouring pixels cast nearly parallel rays from the same
-// eye, so the 64 lanes' gathers fall on few cache lines and the wave's loop
-// trip count (its slowest ray) stays close to its mean ray. Blocks are
-// re-numbered so that each XCD (blocks are dealt to the 8 XCDs round-robin)
-// works on a contiguous run of envs, keeping an env's tiles in one L2.
+// One render is two launches on the caller's stream:
+//   1. ray_tables: per env, the (sin, cos) of its H row pitch angles and W
+//      column yaw angles, and its eye point — all the transcendental work of
+//      ray setup, (H+W) fp64 sincos per env instead of two per ray;
+//   2. the march, in one of two schedules with identical results:
+//      - tiles (default): launch-scheduled waves, each marching 8x8 pixel
+//        tiles with RPL rays per lane in flight at once;
+//      - persistent: a grid that fills the GPU once; each wave keeps 64 ray
+//        slots and refills finished slots with new rays (ray compaction),
+//        pulling 8x8 pixel tiles from per-XCD work counters. It keeps every
+//        lane busy but mixes rays of different depths in one gather, which
+//        costs more cache lines per gather than it saves in idle lanes on
+//        the scenes measured so far, so it is not the default.
+// Blocks are numbered so that each XCD (blocks are dealt to the 8 XCDs
+// round-robin) works on a contiguous run of envs, keeping an env's rays in
+// one L2.
 
 #include <hip/hip_runtime.h>
 #include <hip/hip_fp16.h>
+#include <math.h>
 #include <stdarg.h>
 #include <stdint.h>
-#include <string.h>
 #include <stdio.h>
-#include <math.h>
+#include <string.h>
 
 #include "../../include/sdfr.h"
 
@@ -44,6 +54,16 @@ namespace {
 
 constexpr double kD2R = 3.14159265358979323846 / 180.0;  // np.pi / 180.0 in float64
 constexpr float kD2Rf = (float)kD2R;                      // the fp32 scalar torch multiplies by
+
+// Raw buffer descriptor word 3 for gfx9-family (gfx950) untyped loads.
+constexpr int32_t kRsrcWord3 = 0x00020000;
+// Largest nx+ny+nz the per-workgroup axis tables hold (64 KiB of LDS).
+constexpr int kMaxAxisEntries = 16384;
+// Persistent schedule: 8 tile partitions (one per XCD) plus an exit counter,
+// each in its own 128-byte line.
+constexpr int kParts = 8;
+constexpr int kCtrStride = 32;
+constexpr int kCounterWords = (kParts + 1) * kCtrStride;
 
 // ---------------------------------------------------------------- errors --
 thread_local char g_err[512];
@@ -56,9 +76,9 @@ __attribute__((format(printf, 2, 3))) int32_t fail(int32_t code, const char* fmt
     return code;
 }
 
-// ---------------------------------------------------------------- handle --
 }  // namespace
 
+// ---------------------------------------------------------------- handle --
 struct SdfrGrid {
     SdfrGridDesc desc;
     int32_t store_dtype;   // SDFR_F32 | SDFR_F16
@@ -66,27 +86,56 @@ struct SdfrGrid {
     int32_t bx, by, bz;    // brick counts (BRICK4), else nx, ny, nz
     void* data;            // device copy
     int64_t bytes;
+    uint32_t* counters;    // persistent schedule: tile claim counters + exit counter
+    int32_t schedule;      // SDFR_SCHED_*
+    int32_t refill_lanes;  // persistent schedule: refill when this many lanes are free
+    int32_t rays_per_lane; // tiles schedule: rays each lane marches at once (1, 2, 4)
     int device;
+    int cus;               // compute units of the device
 };
 
 namespace {
 
 // ------------------------------------------------------------ grid access --
-template <int LAYOUT>
-__device__ __forceinline__ uint32_t voxel_index(int ix, int iy, int iz, int nx, int ny,
-                                                int bx, int by) {
-    if constexpr (LAYOUT == SDFR_LAYOUT_LINEAR) {
-        return ((uint32_t)iz * (uint32_t)ny + (uint32_t)iy) * (uint32_t)nx + (uint32_t)ix;
+// Both layouts have a separable byte offset, off(ix,iy,iz) = X(ix) + Y(iy) +
+// Z(iz):
+//   LINEAR  [nz][ny][nx]:          X = ix,  Y = iy*nx,  Z = iz*ny*nx
+//   BRICK4  [bz][by][bx][4][4][4]: X = (ix>>2)*64 + (ix&3)
+//                                  Y = (iy>>2)*bx*64 + (iy&3)*4
+//                                  Z = (iz>>2)*by*bx*64 + (iz&3)*16
+// (in elements, times the element size). Each workgroup keeps the three
+// axis tables in LDS, so a march step forms its gather address with three
+// LDS reads and one add instead of integer multiplies. The gather itself goes
+// through a buffer descriptor: 32-bit offsets, and an offset past the end of
+// the copy reads 0 instead of faulting.
+__device__ __forceinline__ uint32_t axis_offset(int i, int nx, int ny, int layout, int bx, int by,
+                                                int log_elem) {
+    uint32_t e;
+    if (i < nx) {
+        const uint32_t ix = (uint32_t)i;
+        e = layout == SDFR_LAYOUT_LINEAR ? ix : ((ix >> 2) << 6) + (ix & 3u);
+    } else if (i < nx + ny) {
+        const uint32_t iy = (uint32_t)(i - nx);
+        e = layout == SDFR_LAYOUT_LINEAR ? iy * (uint32_t)nx
+                                         : (iy >> 2) * (uint32_t)bx * 64u + (iy & 3u) * 4u;
     } else {
-        uint32_t brick = (((uint32_t)(iz >> 2) * (uint32_t)by) + (uint32_t)(iy >> 2)) * (uint32_t)bx
-                         + (uint32_t)(ix >> 2);
-        uint32_t inner = ((uint32_t)(iz & 3) << 4) | ((uint32_t)(iy & 3) << 2) | (uint32_t)(ix & 3);
-        return (brick << 6) | inner;
+        const uint32_t iz = (uint32_t)(i - nx - ny);
+        e = layout == SDFR_LAYOUT_LINEAR ? iz * (uint32_t)ny * (uint32_t)nx
+                                         : (iz >> 2) * (uint32_t)by * (uint32_t)bx * 64u +
+                                               (iz & 3u) * 16u;
     }
+    return e << log_elem;
 }
 
-__device__ __forceinline__ float load_voxel(const float* g, uint32_t i) { return g[i]; }
-__device__ __forceinline__ float load_voxel(const __half* g, uint32_t i) { return __half2float(g[i]); }
+template <typename GT>
+__device__ __forceinline__ float load_voxel(__amdgpu_buffer_rsrc_t rsrc, uint32_t off) {
+    if constexpr (sizeof(GT) == 2) {
+        const unsigned short h = __builtin_amdgcn_raw_buffer_load_b16(rsrc, off, 0, 0);
+        return __half2float(__ushort_as_half(h));
+    } else {
+        return __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rsrc, off, 0, 0));
+    }
+}
 
 // ------------------------------------------------------------- conversions --
 __device__ __forceinline__ uint16_t f32_to_bf16_rne(float f) {
@@ -133,17 +182,18 @@ __device__ __forceinline__ float pinhole_v(int r, int h, double tan_half) {
     return (float)(tan_half * a);
 }
 
-__device__ __forceinline__ void sincos_f32(float x, float* s, float* c) {
+// (sin x, cos x) of an fp32 angle, each the fp64 value rounded once.
+__device__ __forceinline__ float2 sincos_f32(float x) {
     double sd, cd;
     sincos((double)x, &sd, &cd);
-    *s = (float)sd;
-    *c = (float)cd;
+    return make_float2((float)sd, (float)cd);
 }
 
 // --------------------------------------------------------------- the args --
 struct MarchArgs {
     const void* grid;
-    int nx, ny, nz, bx, by;
+    uint32_t grid_bytes;          // size of the device copy (the descriptor's range)
+    int nx, ny, nz, bx, by, layout;
     float fnx1, fny1, fnz1;       // n-1 as float: the clamp bound
     float mnx, mny, mnz, inv_cell;
     float rng, near, hit_eps, min_step;
@@ -154,11 +204,16 @@ struct MarchArgs {
     const float* yaw; int64_t yaw_stride;
     const float* pitch; int64_t pitch_stride;
     const void* ducked; int64_t ducked_stride; int ducked_dtype;
+    int n_envs;
+    float2* rt;                   // ray tables, rt_stride float2 per env
+    int rt_stride;                // H + W + 4
     void* out; int64_t env_stride;
     int32_t* taps;
     int tiles_x, tiles_per_env;
     int64_t total_tiles;
     int nblocks;
+    uint32_t* counters;           // persistent schedule only
+    int refill_lanes;
 };
 
 // Block b runs on XCD b % 8; give XCD x the x-th contiguous eighth of the
@@ -170,103 +225,346 @@ __device__ __forceinline__ int xcd_logical_block(int b, int nblocks) {
 }
 
 // -------------------------------------------------------------- ray setup --
-struct Ray {
-    float ex, ey, ez, dx, dy, dz;
-};
-
-// Eye and unit direction of ray (n, r, c): vision.py:68-84 (kernel) and
-// :596-624 (the CPU path's _dirs_equiangular / _dirs_pinhole).
-__device__ __forceinline__ Ray make_ray(const MarchArgs& a, int n, int r, int c) {
-    Ray ray;
-    const float ox = a.origin[n * a.origin_stride + 0];
-    const float oy = a.origin[n * a.origin_stride + 1];
-    const float oz = a.origin[n * a.origin_stride + 2];
+// Ray table of env n, entries (float2):
+//   [0, H)       rows:    equiangular (sin, cos) of pitch + poff[r];  pinhole (v[r], 0)
+//   [H, H+W)     columns: equiangular (sin, cos) of yaw + yoff[c];    pinhole (u[c], 0)
+//   H+W, H+W+1   eye: (x, y), (z, 0)
+//   H+W+2, +3    pinhole only: (sin, cos) of the view pitch, of the view yaw
+// (vision.py:68-84 kernel setup; :596-624 the CPU path's _dirs_equiangular
+// and _dirs_pinhole; :499-529 the offset tables.)
+__device__ __forceinline__ float2 table_entry(const MarchArgs& a, int n, int e) {
     const float yr = a.yaw[n * a.yaw_stride] * kD2Rf;
     const float pr = a.pitch[n * a.pitch_stride] * kD2Rf;
-    const bool dk = read_ducked(a.ducked, n * a.ducked_stride, a.ducked_dtype);
-    ray.ex = ox;
-    ray.ey = oy;
-    ray.ez = oz + (dk ? 12.0f : 17.0f);
-    if (a.camera == SDFR_CAM_EQUIANGULAR) {
-        const float yw = yr + equiangular_offset(c, a.W, a.hfov);
-        const float pt = pr + equiangular_offset(r, a.H, a.vfov);
-        float sp, cp, sy, cy;
-        sincos_f32(pt, &sp, &cp);
-        sincos_f32(yw, &sy, &cy);
-        ray.dx = cp * cy;
-        ray.dy = cp * sy;
-        ray.dz = sp;
+    if (e < a.H) {
+        if (a.camera == SDFR_CAM_EQUIANGULAR) return sincos_f32(pr + equiangular_offset(e, a.H, a.vfov));
+        return make_float2(pinhole_v(e, a.H, a.tan_v), 0.0f);
+    }
+    e -= a.H;
+    if (e < a.W) {
+        if (a.camera == SDFR_CAM_EQUIANGULAR) return sincos_f32(yr + equiangular_offset(e, a.W, a.hfov));
+        return make_float2(pinhole_u(e, a.W, a.tan_h), 0.0f);
+    }
+    e -= a.W;
+    if (e == 0) return make_float2(a.origin[n * a.origin_stride + 0], a.origin[n * a.origin_stride + 1]);
+    if (e == 1) {
+        const bool dk = read_ducked(a.ducked, n * a.ducked_stride, a.ducked_dtype);
+        return make_float2(a.origin[n * a.origin_stride + 2] + (dk ? 12.0f : 17.0f), 0.0f);
+    }
+    if (a.camera != SDFR_CAM_PINHOLE) return make_float2(0.0f, 0.0f);
+    return sincos_f32(e == 2 ? pr : yr);
+}
+
+// Unit direction from a ray's row and column entries (and, pinhole, the
+// env's view sin/cos pairs).
+template <int CAMERA>
+__device__ __forceinline__ float3 ray_dir(float2 row, float2 col, float2 pitch_sc, float2 yaw_sc) {
+    if constexpr (CAMERA == SDFR_CAM_EQUIANGULAR) {
+        // row = (sin p, cos p), col = (sin y, cos y)
+        return make_float3(row.y * col.y, row.y * col.x, row.x);
     } else {
-        const float u = pinhole_u(c, a.W, a.tan_h);
-        const float v = pinhole_v(r, a.H, a.tan_v);
-        float sp, cp, sy, cy;
-        sincos_f32(pr, &sp, &cp);
-        sincos_f32(yr, &sy, &cy);
-        // forward + u*right + v*up, then normalised (the CPU path's rsqrt is
-        // 1/sqrt with two fp32 roundings)
+        // forward + u*right + v*up, normalised (vision.py:236-246, :614-624);
+        // the CPU path's rsqrt is 1/sqrt with two fp32 roundings
+        const float v = row.x, u = col.x;
+        const float sp = pitch_sc.x, cp = pitch_sc.y, sy = yaw_sc.x, cy = yaw_sc.y;
         const float px = cp * cy + u * sy - v * sp * cy;
         const float py = cp * sy - u * cy - v * sp * sy;
         const float pz = sp + v * cp;
         const float inv = 1.0f / sqrtf(px * px + py * py + pz * pz);
-        ray.dx = px * inv;
-        ray.dy = py * inv;
-        ray.dz = pz * inv;
+        return make_float3(px * inv, py * inv, pz * inv);
     }
-    return ray;
 }
 
 // The encoding, vision.py:112-116 / :654-657; t already clamped to range.
+// At t <= near the tail is 0.25*(1 - exp(-0)) = 0 exactly, so it is skipped.
 __device__ __forceinline__ float encode_depth(float t, float near) {
-    const float lin = fminf(t, near) / near;
-    const float xe = -fmaxf(t - near, 0.0f) / 2500.0f;
+    if (!(t > near)) return t / near;
+    const float lin = near / near;
+    const float xe = -(t - near) / 2500.0f;
     const float ed = (float)exp((double)xe);
     return lin + 0.25f * (1.0f - ed);
 }
 
-// ------------------------------------------------------------- the kernel --
-template <typename GT, int LAYOUT, int OUT_DTYPE, int TW, int TH, bool CENSUS>
+template <int OUT_DTYPE>
+__device__ __forceinline__ void store_enc(void* out, int64_t o, float enc) {
+    if constexpr (OUT_DTYPE == SDFR_BF16) ((uint16_t*)out)[o] = f32_to_bf16_rne(enc);
+    else ((float*)out)[o] = enc;
+}
+
+// One march step of a live ray (vision.py:101-111). Returns whether the ray
+// is still alive; t advances only if it is.
+template <typename GT>
+__device__ __forceinline__ bool march_step(const MarchArgs& a, __amdgpu_buffer_rsrc_t rsrc,
+                                           const uint32_t* __restrict__ tab, float ex, float ey,
+                                           float ez, float dx, float dy, float dz, float& t) {
+    const float px = ex + dx * t;
+    const float py = ey + dy * t;
+    const float pz = ez + dz * t;
+    const int ix = (int)__builtin_amdgcn_fmed3f((px - a.mnx) * a.inv_cell, 0.0f, a.fnx1);
+    const int iy = (int)__builtin_amdgcn_fmed3f((py - a.mny) * a.inv_cell, 0.0f, a.fny1);
+    const int iz = (int)__builtin_amdgcn_fmed3f((pz - a.mnz) * a.inv_cell, 0.0f, a.fnz1);
+    const float sd = load_voxel<GT>(rsrc, tab[ix] + tab[a.nx + iy] + tab[a.nx + a.ny + iz]);
+    const bool alive = (sd > a.hit_eps) && (t < a.rng);
+    if (alive) t = t + fmaxf(sd * 0.9f, a.min_step);
+    return alive;
+}
+
+template <typename GT, int LAYOUT>
+__device__ __forceinline__ void fill_axis_tables(const MarchArgs& a, uint32_t* s_axis) {
+    constexpr int kLog = sizeof(GT) == 2 ? 1 : 2;
+    const int ntab = a.nx + a.ny + a.nz;
+    for (int i = threadIdx.x; i < ntab; i += blockDim.x)
+        s_axis[i] = axis_offset(i, a.nx, a.ny, LAYOUT, a.bx, a.by, kLog);
+    __syncthreads();
+}
+
+// ------------------------------------------------------------ ray tables --
+__global__ __launch_bounds__(256) void ray_tables_kernel(MarchArgs a) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= (int64_t)a.n_envs * a.rt_stride) return;
+    const int n = (int)(i / a.rt_stride);
+    const int e = (int)(i - (int64_t)n * a.rt_stride);
+    a.rt[i] = table_entry(a, n, e);
+}
+
+// ------------------------------------------------------ schedule: tiles --
+// Each wave64 marches RPL 8x8 pixel tiles of consecutive tile index (so,
+// mostly, neighbouring tiles of one env): lane l holds pixel l of every one
+// of them. Per step a lane issues the gathers of all its live rays before
+// using any, so RPL independent loads per lane are in flight at once — the
+// march is bound by gather latency, and this multiplies the loads in flight
+// without more waves. Lanes of dead rays point their load at offset 0 (all at
+// one address), which costs one cache line per wave-step.
+//
+// The step counter is wave-uniform and the loop leaves as soon as no ray of
+// the wave is alive, which is exact: alive only turns off and a dead ray adds
+// 0 to t.
+template <typename GT, int LAYOUT, int OUT_DTYPE, int CAMERA, bool CENSUS, int RPL>
 __global__ __launch_bounds__(256) void march_tiles(MarchArgs a) {
-    static_assert(TW * TH == 64, "one wave64 per tile");
+    extern __shared__ uint32_t s_axis[];
+    fill_axis_tables<GT, LAYOUT>(a, s_axis);
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int lane = threadIdx.x & 63;
     const int blk = xcd_logical_block(blockIdx.x, a.nblocks);
-    const int64_t tile = (int64_t)blk * 4 + wave;
-    if (tile >= a.total_tiles) return;
-    const int n = (int)(tile / a.tiles_per_env);
-    const int rem = (int)(tile - (int64_t)n * a.tiles_per_env);
-    const int ty = rem / a.tiles_x, tx = rem - ty * a.tiles_x;
-    const int r = ty * TH + lane / TW;
-    const int c = tx * TW + lane % TW;
-    if (r >= a.H || c >= a.W) return;
+    const int64_t tile0 = ((int64_t)blk * 4 + wave) * RPL;
+    if (tile0 >= a.total_tiles) return;
 
-    const Ray ray = make_ray(a, n, r, c);
-    const GT* __restrict__ g = (const GT*)a.grid;
-    float t = 0.0f;
-    int taps = 0;
+    float ex[RPL], ey[RPL], ez[RPL], dx[RPL], dy[RPL], dz[RPL], t[RPL];
+    int64_t o[RPL];
+    int taps[RPL];
+    bool alive[RPL], valid[RPL];
+#pragma unroll
+    for (int j = 0; j < RPL; ++j) {
+        const int64_t tile = tile0 + j;
+        const bool tile_ok = tile < a.total_tiles;
+        const int64_t tl = tile_ok ? tile : tile0;
+        const int n = __builtin_amdgcn_readfirstlane((int)(tl / a.tiles_per_env));
+        const int rem = (int)(tl - (int64_t)n * a.tiles_per_env);
+        const int ty = __builtin_amdgcn_readfirstlane(rem / a.tiles_x);
+        const int tx = __builtin_amdgcn_readfirstlane(rem - ty * a.tiles_x);
+        const int r = ty * 8 + (lane >> 3);
+        const int c = tx * 8 + (lane & 7);
+        valid[j] = tile_ok && r < a.H && c < a.W;
+        const int rr = min(r, a.H - 1), cc = min(c, a.W - 1);
+        const float2* rt = a.rt + (int64_t)n * a.rt_stride;
+        const float2 e01 = rt[a.H + a.W], e2 = rt[a.H + a.W + 1];
+        float2 psc = make_float2(0.f, 0.f), ysc = make_float2(0.f, 0.f);
+        if constexpr (CAMERA == SDFR_CAM_PINHOLE) {
+            psc = rt[a.H + a.W + 2];
+            ysc = rt[a.H + a.W + 3];
+        }
+        const float3 d = ray_dir<CAMERA>(rt[rr], rt[a.H + cc], psc, ysc);
+        ex[j] = e01.x;
+        ey[j] = e01.y;
+        ez[j] = e2.x;
+        dx[j] = d.x;
+        dy[j] = d.y;
+        dz[j] = d.z;
+        t[j] = 0.0f;
+        taps[j] = 0;
+        alive[j] = valid[j];
+        o[j] = (int64_t)n * a.env_stride + (int64_t)rr * a.W + cc;
+    }
+    const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<void*>(a.grid), 0, (int)a.grid_bytes, kRsrcWord3);
+    const uint32_t* __restrict__ tab = s_axis;
     for (int k = 0; k < a.max_steps; ++k) {
-        const float px = ray.ex + ray.dx * t;
-        const float py = ray.ey + ray.dy * t;
-        const float pz = ray.ez + ray.dz * t;
-        const int ix = (int)__builtin_amdgcn_fmed3f((px - a.mnx) * a.inv_cell, 0.0f, a.fnx1);
-        const int iy = (int)__builtin_amdgcn_fmed3f((py - a.mny) * a.inv_cell, 0.0f, a.fny1);
-        const int iz = (int)__builtin_amdgcn_fmed3f((pz - a.mnz) * a.inv_cell, 0.0f, a.fnz1);
-        const float s = load_voxel(g, voxel_index<LAYOUT>(ix, iy, iz, a.nx, a.ny, a.bx, a.by));
-        if constexpr (CENSUS) ++taps;
-        if (!(s > a.hit_eps) || !(t < a.rng)) break;
-        t = t + fmaxf(s * 0.9f, a.min_step);
+        bool any_alive = false;
+#pragma unroll
+        for (int j = 0; j < RPL; ++j) any_alive |= alive[j];
+        if (!__any(any_alive)) break;
+        float sd[RPL];
+#pragma unroll
+        for (int j = 0; j < RPL; ++j) {
+            const float px = ex[j] + dx[j] * t[j];
+            const float py = ey[j] + dy[j] * t[j];
+            const float pz = ez[j] + dz[j] * t[j];
+            const int ix = (int)__builtin_amdgcn_fmed3f((px - a.mnx) * a.inv_cell, 0.0f, a.fnx1);
+            const int iy = (int)__builtin_amdgcn_fmed3f((py - a.mny) * a.inv_cell, 0.0f, a.fny1);
+            const int iz = (int)__builtin_amdgcn_fmed3f((pz - a.mnz) * a.inv_cell, 0.0f, a.fnz1);
+            const uint32_t off = alive[j] ? tab[ix] + tab[a.nx + iy] + tab[a.nx + a.ny + iz] : 0u;
+            sd[j] = load_voxel<GT>(rsrc, off);
+        }
+#pragma unroll
+        for (int j = 0; j < RPL; ++j) {
+            if (alive[j]) {
+                if constexpr (CENSUS) ++taps[j];
+                alive[j] = (sd[j] > a.hit_eps) && (t[j] < a.rng);
+                if (alive[j]) t[j] = t[j] + fmaxf(sd[j] * 0.9f, a.min_step);
+            }
+        }
     }
-    const float enc = encode_depth(fminf(t, a.rng), a.near);
-
-    const int64_t o = (int64_t)n * a.env_stride + (int64_t)r * a.W + c;
-    if constexpr (OUT_DTYPE == SDFR_BF16) {
-        ((uint16_t*)a.out)[o] = f32_to_bf16_rne(enc);
-    } else {
-        ((float*)a.out)[o] = enc;
+#pragma unroll
+    for (int j = 0; j < RPL; ++j) {
+        if (valid[j]) {
+            store_enc<OUT_DTYPE>(a.out, o[j], encode_depth(fminf(t[j], a.rng), a.near));
+            if constexpr (CENSUS) {
+                const int64_t n = (o[j] - (o[j] % a.env_stride)) / a.env_stride;
+                const int64_t rc = o[j] - n * a.env_stride;
+                a.taps[n * a.H * a.W + rc] = taps[j];
+            }
+        }
     }
-    if constexpr (CENSUS) a.taps[((int64_t)n * a.H + r) * a.W + c] = taps;
 }
 
-// One thread per ray: the directions make_ray() casts, (N,H,W,3) f32.
+// ------------------------------------------------- schedule: persistent --
+// A grid that fills every CU once. Each wave keeps 64 independent ray slots;
+// a slot whose ray has ended is refilled with the next unstarted ray of the
+// wave's tile stream, so a wave no longer idles while its slowest ray
+// finishes (ray refill, after Aila & Laine 2009). Refills are batched: they
+// run when at least refill_lanes slots are free, one ballot and one prefix
+// count (mbcnt) hand out the new rays, and the outputs of the rays that ended
+// are written in the same batch.
+//
+// Tile stream: 8 partitions of the tiles (one per XCD: block b runs on XCD
+// b % 8), each a contiguous range of envs, claimed one tile at a time with an
+// atomic counter; the next claim is issued as soon as a tile is taken, so its
+// latency overlaps the march. A wave whose partition is drained moves on to
+// the next one. The last wave to leave resets the counters (no other wave
+// touches them after that point), so launches on one stream, and graph
+// replays, need no clearing in between.
+__device__ __forceinline__ uint32_t claim_raw(const MarchArgs& a, int part, int lane) {
+    uint32_t got = 0;
+    if (lane == 0) got = atomicAdd(&a.counters[part * kCtrStride], 1u);
+    return got;
+}
+
+template <typename GT, int LAYOUT, int OUT_DTYPE, int CAMERA, bool CENSUS>
+__global__ __launch_bounds__(256) void march_persistent(MarchArgs a) {
+    extern __shared__ uint32_t s_axis[];
+    fill_axis_tables<GT, LAYOUT>(a, s_axis);
+    const int lane = threadIdx.x & 63;
+    const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<void*>(a.grid), 0, (int)a.grid_bytes, kRsrcWord3);
+
+    int part = (int)((int64_t)xcd_logical_block(blockIdx.x, a.nblocks) * kParts / a.nblocks);
+    uint32_t pending = claim_raw(a, part, lane);   // raw claim on `part`, checked when needed
+    int tiles_tried = 0;
+    bool more = true;     // the tile stream may still have tiles
+    int tn = 0, tr0 = 0, tc0 = 0;   // the tile being handed out
+    int pos = 64;         // next unstarted ray in it (64 = none left)
+
+    // per-lane ray
+    float ex = 0.f, ey = 0.f, ez = 0.f, dx = 0.f, dy = 0.f, dz = 0.f, t = 0.f;
+    int k = 0;
+    int64_t o = 0;        // output element of the ray
+    int32_t pix = 0;      // n*H*W + r*W + c, for the census
+    bool has = false;     // the slot holds a ray (running or ended, not yet written)
+    bool alive = false;   // ... and it is still marching
+
+    while (true) {
+        const int n_free = 64 - (int)__popcll(__ballot(alive));
+        if (n_free >= a.refill_lanes || n_free == 64) {
+            // write the rays that ended since the last batch
+            if (has && !alive) {
+                store_enc<OUT_DTYPE>(a.out, o, encode_depth(fminf(t, a.rng), a.near));
+                if constexpr (CENSUS) a.taps[pix] = k;
+                has = false;
+            }
+            // hand new rays to the free slots, from at most two tiles
+            for (int round = 0; round < 2 && more; ++round) {
+                if (pos >= 64) {
+                    // take the pending claim, walking on to the next partition when drained
+                    int64_t tile = -1;
+                    while (true) {
+                        const int64_t lo = a.total_tiles * part / kParts;
+                        const int64_t hi = a.total_tiles * (part + 1) / kParts;
+                        const uint32_t got = __builtin_amdgcn_readfirstlane(pending);
+                        if (lo + (int64_t)got < hi) {
+                            tile = lo + (int64_t)got;
+                            break;
+                        }
+                        if (++tiles_tried >= kParts) break;
+                        part = (part + 1) & (kParts - 1);
+                        pending = claim_raw(a, part, lane);
+                    }
+                    if (tile < 0) {
+                        more = false;
+                        break;
+                    }
+                    pending = claim_raw(a, part, lane);   // next claim, in flight meanwhile
+                    tn = (int)(tile / a.tiles_per_env);
+                    const int rem = (int)(tile - (int64_t)tn * a.tiles_per_env);
+                    const int ty = rem / a.tiles_x;
+                    tr0 = ty * 8;
+                    tc0 = (rem - ty * a.tiles_x) * 8;
+                    pos = 0;
+                }
+                const uint64_t free_mask = __ballot(!has);
+                const int n_give = min((int)__popcll(free_mask), 64 - pos);
+                if (n_give == 0) break;
+                const int rank = __builtin_amdgcn_mbcnt_hi((uint32_t)(free_mask >> 32),
+                                 __builtin_amdgcn_mbcnt_lo((uint32_t)free_mask, 0u));
+                if (!has && rank < n_give) {
+                    const int q = pos + rank;
+                    const int r = tr0 + (q >> 3), c = tc0 + (q & 7);
+                    if (r < a.H && c < a.W) {
+                        const float2* rt = a.rt + (int64_t)tn * a.rt_stride;
+                        const float2 e01 = rt[a.H + a.W], e2 = rt[a.H + a.W + 1];
+                        float2 psc = make_float2(0.f, 0.f), ysc = make_float2(0.f, 0.f);
+                        if constexpr (CAMERA == SDFR_CAM_PINHOLE) {
+                            psc = rt[a.H + a.W + 2];
+                            ysc = rt[a.H + a.W + 3];
+                        }
+                        const float3 d = ray_dir<CAMERA>(rt[r], rt[a.H + c], psc, ysc);
+                        dx = d.x;
+                        dy = d.y;
+                        dz = d.z;
+                        ex = e01.x;
+                        ey = e01.y;
+                        ez = e2.x;
+                        o = (int64_t)tn * a.env_stride + (int64_t)r * a.W + c;
+                        pix = (tn * a.H + r) * a.W + c;
+                        t = 0.0f;
+                        k = 0;
+                        has = true;
+                        alive = a.max_steps > 0;
+                    }
+                }
+                pos += n_give;
+            }
+            if (!more && __ballot(has) == 0) break;
+        }
+        if (alive) {
+            alive = march_step<GT>(a, rsrc, s_axis, ex, ey, ez, dx, dy, dz, t);
+            ++k;
+            alive = alive && k < a.max_steps;
+        }
+    }
+    // the last wave out clears the counters for the next launch
+    if (lane == 0) {
+        const uint32_t total = gridDim.x * (blockDim.x >> 6);
+        const uint32_t done = atomicAdd(&a.counters[kParts * kCtrStride], 1u);
+        if (done == total - 1) {
+            for (int p = 0; p < kParts; ++p) atomicExch(&a.counters[p * kCtrStride], 0u);
+            atomicExch(&a.counters[kParts * kCtrStride], 0u);
+        }
+    }
+}
+
+// ----------------------------------------------------------- directions --
+// One thread per ray: the directions the march casts, (N,H,W,3) f32, from the
+// same table entries and the same ray_dir().
+template <int CAMERA>
 __global__ __launch_bounds__(256) void ray_dirs_kernel(MarchArgs a, float* dirs, int64_t total) {
     const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= total) return;
@@ -274,10 +572,15 @@ __global__ __launch_bounds__(256) void ray_dirs_kernel(MarchArgs a, float* dirs,
     const int n = (int)(i / hw);
     const int pix = (int)(i - (int64_t)n * hw);
     const int r = pix / a.W, c = pix - r * a.W;
-    const Ray ray = make_ray(a, n, r, c);
-    dirs[3 * i + 0] = ray.dx;
-    dirs[3 * i + 1] = ray.dy;
-    dirs[3 * i + 2] = ray.dz;
+    float2 psc = make_float2(0.f, 0.f), ysc = make_float2(0.f, 0.f);
+    if constexpr (CAMERA == SDFR_CAM_PINHOLE) {
+        psc = table_entry(a, n, a.H + a.W + 2);
+        ysc = table_entry(a, n, a.H + a.W + 3);
+    }
+    const float3 d = ray_dir<CAMERA>(table_entry(a, n, r), table_entry(a, n, a.H + c), psc, ysc);
+    dirs[3 * i + 0] = d.x;
+    dirs[3 * i + 1] = d.y;
+    dirs[3 * i + 2] = d.z;
 }
 
 // ------------------------------------------------------------- grid build --
@@ -327,20 +630,48 @@ hipError_t launch_relayout(const void* src, void* dst, const SdfrGrid* g, int64_
 }
 
 // --------------------------------------------------------- render dispatch --
-template <typename GT, int LAYOUT, int OUT, bool CENSUS>
-void launch_march(const MarchArgs& a, hipStream_t st) {
-    march_tiles<GT, LAYOUT, OUT, 8, 8, CENSUS><<<a.nblocks, 256, 0, st>>>(a);
+size_t axis_lds_bytes(const MarchArgs& a) {
+    return sizeof(uint32_t) * (size_t)(a.nx + a.ny + a.nz);
+}
+
+template <typename GT, int LAYOUT, int OUT, int CAMERA, bool CENSUS>
+void launch_march(MarchArgs& a, const SdfrGrid* g, hipStream_t st) {
+    const size_t lds = axis_lds_bytes(a);
+    if (g->schedule == SDFR_SCHED_TILES) {
+        const int rpl = g->rays_per_lane;
+        a.nblocks = (int)((a.total_tiles + 4 * rpl - 1) / (4 * rpl));
+        if (rpl == 4) march_tiles<GT, LAYOUT, OUT, CAMERA, CENSUS, 4><<<a.nblocks, 256, lds, st>>>(a);
+        else if (rpl == 2) march_tiles<GT, LAYOUT, OUT, CAMERA, CENSUS, 2><<<a.nblocks, 256, lds, st>>>(a);
+        else march_tiles<GT, LAYOUT, OUT, CAMERA, CENSUS, 1><<<a.nblocks, 256, lds, st>>>(a);
+        return;
+    }
+    // a grid that fills every CU once, never more blocks than the tiles need
+    int per_cu = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(
+            &per_cu, reinterpret_cast<const void*>(march_persistent<GT, LAYOUT, OUT, CAMERA, CENSUS>),
+            256, lds) != hipSuccess || per_cu <= 0)
+        per_cu = 1;
+    const int64_t want = (int64_t)per_cu * (g->cus > 0 ? g->cus : 1);
+    const int64_t need = (a.total_tiles + 3) / 4;
+    a.nblocks = (int)(want < need ? want : need);
+    march_persistent<GT, LAYOUT, OUT, CAMERA, CENSUS><<<a.nblocks, 256, lds, st>>>(a);
+}
+
+template <typename GT, int LAYOUT, int OUT>
+void dispatch_cam(MarchArgs& a, const SdfrGrid* g, bool census, hipStream_t st) {
+    if (a.camera == SDFR_CAM_PINHOLE) {
+        if (census) launch_march<GT, LAYOUT, OUT, SDFR_CAM_PINHOLE, true>(a, g, st);
+        else launch_march<GT, LAYOUT, OUT, SDFR_CAM_PINHOLE, false>(a, g, st);
+    } else {
+        if (census) launch_march<GT, LAYOUT, OUT, SDFR_CAM_EQUIANGULAR, true>(a, g, st);
+        else launch_march<GT, LAYOUT, OUT, SDFR_CAM_EQUIANGULAR, false>(a, g, st);
+    }
 }
 
 template <typename GT, int LAYOUT>
-void dispatch_out(const MarchArgs& a, int out_dtype, bool census, hipStream_t st) {
-    if (out_dtype == SDFR_BF16) {
-        if (census) launch_march<GT, LAYOUT, SDFR_BF16, true>(a, st);
-        else launch_march<GT, LAYOUT, SDFR_BF16, false>(a, st);
-    } else {
-        if (census) launch_march<GT, LAYOUT, SDFR_F32, true>(a, st);
-        else launch_march<GT, LAYOUT, SDFR_F32, false>(a, st);
-    }
+void dispatch_out(MarchArgs& a, const SdfrGrid* g, int out_dtype, bool census, hipStream_t st) {
+    if (out_dtype == SDFR_BF16) dispatch_cam<GT, LAYOUT, SDFR_BF16>(a, g, census, st);
+    else dispatch_cam<GT, LAYOUT, SDFR_F32>(a, g, census, st);
 }
 
 bool dtype_ok_for_ducked(int d) {
@@ -368,6 +699,9 @@ int32_t check_cam_poses(const char* fn, const SdfrCam* cam, const SdfrPoses* pos
     if (cam->camera != SDFR_CAM_EQUIANGULAR && cam->camera != SDFR_CAM_PINHOLE)
         return fail(-3, "%s: unknown camera model %d", fn, cam->camera);
     if (poses->n_envs <= 0) return fail(-2, "%s: n_envs must be >= 1 (got %d)", fn, poses->n_envs);
+    if ((int64_t)cam->width * cam->height * poses->n_envs > 0x7fffffffLL)
+        return fail(-2, "%s: too many rays (%lld, limit 2^31-1)", fn,
+                    (long long)cam->width * cam->height * poses->n_envs);
     if (!poses->origin || !poses->yaw_deg || !poses->pitch_deg || !poses->ducked)
         return fail(-1, "%s: null pose pointer", fn);
     if (!dtype_ok_for_ducked(poses->ducked_dtype))
@@ -398,6 +732,12 @@ void fill_args(MarchArgs* a, const SdfrCam* cam, const SdfrPoses* poses) {
     a->ducked = poses->ducked;
     a->ducked_stride = poses->ducked_stride;
     a->ducked_dtype = poses->ducked_dtype;
+    a->n_envs = poses->n_envs;
+    a->rt_stride = cam->width + cam->height + 4;
+}
+
+int64_t workspace_bytes(int width, int height, int n_envs) {
+    return (int64_t)n_envs * (width + height + 4) * (int64_t)sizeof(float2);
 }
 
 }  // namespace
@@ -410,6 +750,13 @@ SDFR_API int32_t sdfr_abi_version(void) { return SDFR_ABI_VERSION; }
 SDFR_API const char* sdfr_last_error(void) { return g_err; }
 
 SDFR_API int64_t sdfr_grid_bytes(const SdfrGrid* grid) { return grid ? grid->bytes : -1; }
+
+SDFR_API int64_t sdfr_workspace_bytes(const SdfrCam* cam, int32_t n_envs) {
+    g_err[0] = '\0';
+    if (!cam || cam->width <= 0 || cam->height <= 0 || n_envs <= 0)
+        return fail(-2, "sdfr_workspace_bytes: need a camera with positive size and n_envs >= 1");
+    return workspace_bytes(cam->width, cam->height, n_envs);
+}
 
 SDFR_API SdfrGrid* sdfr_grid_create(const SdfrGridDesc* desc, const void* src, int32_t src_dtype,
                                     int32_t src_on_device, int32_t store_dtype, int32_t layout,
@@ -455,8 +802,14 @@ SDFR_API SdfrGrid* sdfr_grid_create(const SdfrGridDesc* desc, const void* src, i
         bz = (desc->nz + 3) / 4;
         count = (int64_t)bx * by * bz * 64;
     }
-    if (count >= ((int64_t)1 << 32)) {
-        fail(-2, "sdfr_grid_create: grid too large (%lld voxels, limit 2^32)", (long long)count);
+    // The kernels address the copy with 32-bit byte offsets through a buffer
+    // descriptor, summed from per-axis tables held in LDS (axis_offset).
+    const int64_t elem = store_dtype == SDFR_F16 ? 2 : 4;
+    if (count * elem > (int64_t)0xffffffffLL ||
+        (int64_t)desc->nx + desc->ny + desc->nz > kMaxAxisEntries) {
+        fail(-2, "sdfr_grid_create: grid too large (%d x %d x %d, %lld bytes; limits: 4 GiB and "
+             "nx+ny+nz <= %d)", desc->nx, desc->ny, desc->nz, (long long)(count * elem),
+             kMaxAxisEntries);
         copy_err(err, errlen);
         return nullptr;
     }
@@ -469,14 +822,23 @@ SDFR_API SdfrGrid* sdfr_grid_create(const SdfrGridDesc* desc, const void* src, i
     g->bx = bx;
     g->by = by;
     g->bz = bz;
-    g->bytes = count * (store_dtype == SDFR_F16 ? 2 : 4);
+    g->bytes = count * elem;
     g->data = nullptr;
-    (void)hipGetDevice(&g->device);
+    g->counters = nullptr;
+    g->schedule = SDFR_SCHED_TILES;
+    g->refill_lanes = 16;
+    g->rays_per_lane = 2;
+    g->cus = 0;
+    hipError_t e = hipGetDevice(&g->device);
+    if (e == hipSuccess)
+        e = hipDeviceGetAttribute(&g->cus, hipDeviceAttributeMultiprocessorCount, g->device);
 
     const int64_t src_bytes = nvox * (src_dtype == SDFR_F16 ? 2 : 4);
     void* staged = nullptr;
     const void* dsrc = src;
-    hipError_t e = hipMalloc(&g->data, (size_t)g->bytes);
+    if (e == hipSuccess) e = hipMalloc(&g->data, (size_t)g->bytes);
+    if (e == hipSuccess) e = hipMalloc((void**)&g->counters, sizeof(uint32_t) * kCounterWords);
+    if (e == hipSuccess) e = hipMemsetAsync(g->counters, 0, sizeof(uint32_t) * kCounterWords, st);
     if (e == hipSuccess && !src_on_device) {
         e = hipMalloc(&staged, (size_t)src_bytes);
         if (e == hipSuccess)
@@ -499,6 +861,7 @@ SDFR_API SdfrGrid* sdfr_grid_create(const SdfrGridDesc* desc, const void* src, i
         fail(-4, "sdfr_grid_create: HIP error %s", hipGetErrorString(e));
         copy_err(err, errlen);
         if (g->data) (void)hipFree(g->data);
+        if (g->counters) (void)hipFree(g->counters);
         delete g;
         return nullptr;
     }
@@ -508,11 +871,31 @@ SDFR_API SdfrGrid* sdfr_grid_create(const SdfrGridDesc* desc, const void* src, i
 SDFR_API void sdfr_grid_destroy(SdfrGrid* grid) {
     if (!grid) return;
     if (grid->data) (void)hipFree(grid->data);
+    if (grid->counters) (void)hipFree(grid->counters);
     delete grid;
 }
 
+SDFR_API int32_t sdfr_grid_set_schedule(SdfrGrid* grid, int32_t schedule, int32_t refill_lanes,
+                                        int32_t rays_per_lane) {
+    g_err[0] = '\0';
+    if (!grid) return fail(-1, "sdfr_grid_set_schedule: null grid handle");
+    if (schedule != SDFR_SCHED_PERSISTENT && schedule != SDFR_SCHED_TILES)
+        return fail(-3, "sdfr_grid_set_schedule: unknown schedule %d", schedule);
+    if (refill_lanes < 1 || refill_lanes > 64)
+        return fail(-2, "sdfr_grid_set_schedule: refill_lanes must be in 1..64 (got %d)",
+                    refill_lanes);
+    if (rays_per_lane != 1 && rays_per_lane != 2 && rays_per_lane != 4)
+        return fail(-2, "sdfr_grid_set_schedule: rays_per_lane must be 1, 2 or 4 (got %d)",
+                    rays_per_lane);
+    grid->schedule = schedule;
+    grid->refill_lanes = refill_lanes;
+    grid->rays_per_lane = rays_per_lane;
+    return 0;
+}
+
 SDFR_API int32_t sdfr_render(const SdfrGrid* grid, const SdfrCam* cam, const SdfrPoses* poses,
-                             const SdfrImage* image, void* stream) {
+                             const SdfrImage* image, void* workspace, int64_t workspace_size,
+                             void* stream) {
     g_err[0] = '\0';
     if (!grid || !grid->data) return fail(-1, "sdfr_render: null grid handle");
     if (!image) return fail(-1, "sdfr_render: null image argument");
@@ -524,15 +907,24 @@ SDFR_API int32_t sdfr_render(const SdfrGrid* grid, const SdfrCam* cam, const Sdf
     if (image->env_stride < (int64_t)cam->width * cam->height)
         return fail(-2, "sdfr_render: env_stride %lld is smaller than H*W",
                     (long long)image->env_stride);
+    const int64_t need = workspace_bytes(cam->width, cam->height, poses->n_envs);
+    if (!workspace || workspace_size < need)
+        return fail(-2, "sdfr_render: workspace of %lld bytes needed (got %lld)", (long long)need,
+                    (long long)workspace_size);
+    if (((uintptr_t)workspace & 7u) != 0)
+        return fail(-2, "sdfr_render: workspace must be 8-byte aligned");
 
     MarchArgs a;
     fill_args(&a, cam, poses);
+    a.rt = (float2*)workspace;
     a.grid = grid->data;
+    a.grid_bytes = (uint32_t)grid->bytes;
     a.nx = grid->desc.nx;
     a.ny = grid->desc.ny;
     a.nz = grid->desc.nz;
     a.bx = grid->bx;
     a.by = grid->by;
+    a.layout = grid->layout;
     a.fnx1 = (float)(grid->desc.nx - 1);
     a.fny1 = (float)(grid->desc.ny - 1);
     a.fnz1 = (float)(grid->desc.nz - 1);
@@ -543,6 +935,8 @@ SDFR_API int32_t sdfr_render(const SdfrGrid* grid, const SdfrCam* cam, const Sdf
     a.out = image->out;
     a.env_stride = image->env_stride;
     a.taps = image->taps;
+    a.counters = grid->counters;
+    a.refill_lanes = grid->refill_lanes;
     a.tiles_x = (cam->width + 7) / 8;
     a.tiles_per_env = a.tiles_x * ((cam->height + 7) / 8);
     a.total_tiles = (int64_t)a.tiles_per_env * poses->n_envs;
@@ -552,17 +946,19 @@ SDFR_API int32_t sdfr_render(const SdfrGrid* grid, const SdfrCam* cam, const Sdf
     a.nblocks = (int)nblocks;
 
     hipStream_t st = (hipStream_t)stream;
+    const int64_t entries = (int64_t)poses->n_envs * a.rt_stride;
+    ray_tables_kernel<<<(int)((entries + 255) / 256), 256, 0, st>>>(a);
     const bool census = image->taps != nullptr;
     if (grid->store_dtype == SDFR_F16) {
         if (grid->layout == SDFR_LAYOUT_BRICK4)
-            dispatch_out<__half, SDFR_LAYOUT_BRICK4>(a, image->dtype, census, st);
+            dispatch_out<__half, SDFR_LAYOUT_BRICK4>(a, grid, image->dtype, census, st);
         else
-            dispatch_out<__half, SDFR_LAYOUT_LINEAR>(a, image->dtype, census, st);
+            dispatch_out<__half, SDFR_LAYOUT_LINEAR>(a, grid, image->dtype, census, st);
     } else {
         if (grid->layout == SDFR_LAYOUT_BRICK4)
-            dispatch_out<float, SDFR_LAYOUT_BRICK4>(a, image->dtype, census, st);
+            dispatch_out<float, SDFR_LAYOUT_BRICK4>(a, grid, image->dtype, census, st);
         else
-            dispatch_out<float, SDFR_LAYOUT_LINEAR>(a, image->dtype, census, st);
+            dispatch_out<float, SDFR_LAYOUT_LINEAR>(a, grid, image->dtype, census, st);
     }
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return fail(-4, "sdfr_render: launch failed: %s", hipGetErrorString(e));
@@ -579,8 +975,10 @@ SDFR_API int32_t sdfr_ray_dirs(const SdfrCam* cam, const SdfrPoses* poses, float
     fill_args(&a, cam, poses);
     const int64_t total = (int64_t)cam->width * cam->height * poses->n_envs;
     const int64_t blocks = (total + 255) / 256;
-    if (blocks > 0x7fffffff) return fail(-2, "sdfr_ray_dirs: too many rays (%lld)", (long long)total);
-    ray_dirs_kernel<<<(int)blocks, 256, 0, (hipStream_t)stream>>>(a, dirs, total);
+    if (cam->camera == SDFR_CAM_PINHOLE)
+        ray_dirs_kernel<SDFR_CAM_PINHOLE><<<(int)blocks, 256, 0, (hipStream_t)stream>>>(a, dirs, total);
+    else
+        ray_dirs_kernel<SDFR_CAM_EQUIANGULAR><<<(int)blocks, 256, 0, (hipStream_t)stream>>>(a, dirs, total);
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return fail(-4, "sdfr_ray_dirs: launch failed: %s", hipGetErrorString(e));
     return 0;

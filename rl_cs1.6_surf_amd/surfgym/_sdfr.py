@@ -18,15 +18,17 @@ import torch  # noqa: F401  (load torch's HIP runtime first, see above)
 PKG_ROOT = Path(__file__).resolve().parents[1]
 LIB_PATH = PKG_ROOT / "lib" / "libsdfr.so"
 
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 # element types (SDFR_* in sdfr.h)
 F32, F16, BF16, I32, I64, U8, F64 = 0, 1, 2, 3, 4, 5, 6
 LAYOUT_LINEAR, LAYOUT_BRICK4 = 0, 1
 CAM_EQUIANGULAR, CAM_PINHOLE = 0, 1
+SCHED_PERSISTENT, SCHED_TILES = 0, 1
 
 EXPORTS = ("sdfr_abi_version", "sdfr_last_error", "sdfr_grid_create", "sdfr_grid_destroy",
-           "sdfr_grid_bytes", "sdfr_render", "sdfr_ray_dirs")
+           "sdfr_grid_bytes", "sdfr_grid_set_schedule", "sdfr_workspace_bytes", "sdfr_render",
+           "sdfr_ray_dirs")
 
 
 class GridDesc(ctypes.Structure):
@@ -86,9 +88,13 @@ def load(path: Path | str | None = None):
     lib.sdfr_grid_destroy.argtypes = [vp]
     lib.sdfr_grid_bytes.restype = i64
     lib.sdfr_grid_bytes.argtypes = [vp]
+    lib.sdfr_grid_set_schedule.restype = i32
+    lib.sdfr_grid_set_schedule.argtypes = [vp, i32, i32, i32]
+    lib.sdfr_workspace_bytes.restype = i64
+    lib.sdfr_workspace_bytes.argtypes = [ctypes.POINTER(Cam), i32]
     lib.sdfr_render.restype = i32
     lib.sdfr_render.argtypes = [vp, ctypes.POINTER(Cam), ctypes.POINTER(Poses),
-                                ctypes.POINTER(Image), vp]
+                                ctypes.POINTER(Image), vp, i64, vp]
     lib.sdfr_ray_dirs.restype = i32
     lib.sdfr_ray_dirs.argtypes = [ctypes.POINTER(Cam), ctypes.POINTER(Poses), vp, vp]
     got = lib.sdfr_abi_version()

@@ -45,6 +45,7 @@ _DUCK_DTYPES = {torch.float32: _sdfr.F32, torch.float16: _sdfr.F16, torch.bfloat
 _GRID_DTYPES = {torch.float32: _sdfr.F32, torch.float16: _sdfr.F16}
 _OUT_DTYPES = {torch.float32: _sdfr.F32, torch.bfloat16: _sdfr.BF16}
 _LAYOUTS = {"linear": _sdfr.LAYOUT_LINEAR, "brick4": _sdfr.LAYOUT_BRICK4}
+_SCHEDULES = {"persistent": _sdfr.SCHED_PERSISTENT, "tiles": _sdfr.SCHED_TILES}
 
 
 def pick_cell(core, budget_voxels: float = 700e6) -> float:
@@ -112,7 +113,12 @@ class GpuLidar:
     * ``layout`` — the device copy's order, "brick4" (4x4x4 bricks) or
       "linear";
     * ``hit_eps`` / ``min_step`` — the step rule's constants, 0.6*cell and
-      0.3*cell by default (vision.py:87-88).
+      0.3*cell by default (vision.py:87-88);
+    * ``schedule`` / ``refill_lanes`` / ``rays_per_lane`` — how the kernel
+      schedules rays: launch-scheduled waves of 8x8 pixel "tiles", each lane
+      marching ``rays_per_lane`` rays at once (default, 2), or "persistent"
+      waves that refill lanes with new rays once ``refill_lanes`` of them
+      have finished. The results are identical.
     """
 
     def __init__(self, core, width: int = 128, height: int = 64,
@@ -122,7 +128,8 @@ class GpuLidar:
                  device="cuda", surf_mask: bool = False,
                  pinhole: bool = False, *, grid_dtype=torch.float16,
                  layout: str = "brick4", hit_eps: float = None,
-                 min_step: float = None, _grid=None) -> None:
+                 min_step: float = None, schedule: str = "tiles",
+                 refill_lanes: int = 16, rays_per_lane: int = 2, _grid=None) -> None:
         if surf_mask and pinhole:
             raise ValueError(
                 "surf_mask and pinhole are separate experiments and there is "
@@ -139,6 +146,8 @@ class GpuLidar:
             raise ValueError(f"grid_dtype must be torch.float16 or torch.float32, got {grid_dtype}")
         if layout not in _LAYOUTS:
             raise ValueError(f"layout must be one of {sorted(_LAYOUTS)}, got {layout!r}")
+        if schedule not in _SCHEDULES:
+            raise ValueError(f"schedule must be one of {sorted(_SCHEDULES)}, got {schedule!r}")
         self._lib = _sdfr.load()
         sdf, mins, cell = _grid if _grid is not None else build_sdf(core, cell)
         sdf = np.asarray(sdf)
@@ -195,6 +204,18 @@ class GpuLidar:
         if not h:
             raise _sdfr.SdfrError(err.value.decode("utf-8", "replace"))
         self._grid = h
+        self.set_schedule(schedule, refill_lanes, rays_per_lane)
+
+    def set_schedule(self, schedule: str = "tiles", refill_lanes: int = 16,
+                     rays_per_lane: int = 2) -> None:
+        """Switch the ray schedule of later renders (results are unchanged)."""
+        if schedule not in _SCHEDULES:
+            raise ValueError(f"schedule must be one of {sorted(_SCHEDULES)}, got {schedule!r}")
+        _sdfr.check(self._lib.sdfr_grid_set_schedule(self._grid, _SCHEDULES[schedule],
+                                                     int(refill_lanes), int(rays_per_lane)),
+                    "sdfr_grid_set_schedule", self._lib)
+        self.schedule, self.refill_lanes = schedule, int(refill_lanes)
+        self.rays_per_lane = int(rays_per_lane)
 
     @classmethod
     def from_grid(cls, sdf, mins, cell, **kwargs) -> "GpuLidar":
@@ -214,6 +235,19 @@ class GpuLidar:
             self._lib.sdfr_grid_destroy(h)
 
     # ------------------------------------------------------------------ args --
+    def _workspace(self, cam, n: int) -> torch.Tensor:
+        """The render's ray-table scratch, kept and grown with N. It is
+        allocated outside the render call, so a render captured into a graph
+        after one eager render of the same N allocates nothing."""
+        need = int(self._lib.sdfr_workspace_bytes(ctypes.byref(cam), n))
+        if need < 0:
+            _sdfr.check(need, "sdfr_workspace_bytes", self._lib)
+        ws = getattr(self, "_ws", None)
+        if ws is None or ws.numel() < need:
+            ws = torch.empty(need, dtype=torch.uint8, device=self.device)
+            self._ws = ws
+        return ws
+
     def _cam(self) -> _sdfr.Cam:
         return _sdfr.Cam(self.W, self.H, self.hfov_deg, self.vfov_deg, self._tan_h, self._tan_v,
                          self.range, self.near, self.hit_eps, self.min_step, self.max_steps,
@@ -289,10 +323,12 @@ class GpuLidar:
                 raise ValueError("taps must be a contiguous int32 (N,H,W) tensor on the device")
             taps_ptr = taps.data_ptr()
         img = _sdfr.Image(out.data_ptr(), env_stride, _OUT_DTYPES[out.dtype], 0, taps_ptr)
+        cam = self._cam()
+        ws = self._workspace(cam, n)
         with torch.cuda.device(self.device):
             stream = torch.cuda.current_stream(self.device).cuda_stream
-            rc = self._lib.sdfr_render(self._grid, ctypes.byref(self._cam()), ctypes.byref(poses),
-                                       ctypes.byref(img), stream)
+            rc = self._lib.sdfr_render(self._grid, ctypes.byref(cam), ctypes.byref(poses),
+                                       ctypes.byref(img), ws.data_ptr(), ws.numel(), stream)
         _sdfr.check(rc, "sdfr_render", self._lib)
         del keep
         return out

@@ -101,8 +101,10 @@ def test_render_rejects_bad_arguments_without_a_device():
     lib = _sdfr.load()
     img = _sdfr.Image(64, 128 * 64, _sdfr.F32, 0, None)
     rc = lib.sdfr_render(None, ctypes.byref(_cam()), ctypes.byref(_poses()), ctypes.byref(img),
-                         None)
+                         None, 0, None)
     assert rc == -1 and "grid" in _sdfr.last_error()
+    assert lib.sdfr_workspace_bytes(ctypes.byref(_cam()), 2048) == 2048 * (128 + 64 + 4) * 8
+    assert lib.sdfr_workspace_bytes(ctypes.byref(_cam()), 0) < 0
     # the grid check comes first; the argument checks are shared with sdfr_ray_dirs
     cases = [
         (dict(width=0), {}, "image size"),
