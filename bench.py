@@ -68,6 +68,19 @@ def cpu_baseline(w, sc, envs, repeats=3):
                       f"median of {repeats}: {t * 1e3:.1f} ms; cpu: {model}"}
 
 
+def profiled_traffic(key):
+    """L2-miss traffic per launch recorded for this configuration by the
+    FETCH_SIZE / WRITE_SIZE counter runs summarised under profiles/ (a line
+    ``traffic_bytes_per_launch[<key>] = <bytes>``), or None."""
+    import re
+    for f in sorted((ROOT / "profiles").glob("*.md")):
+        for line in f.read_text().splitlines():
+            m = re.match(r"traffic_bytes_per_launch\[(.+?)\] = (\d+)", line.strip())
+            if m and m.group(1) == key:
+                return int(m.group(2))
+    return None
+
+
 def copy_bandwidth(dev, n_bytes=2_000_000_000, iters=10):
     """Device copy bandwidth, 2 x bytes / time (read + write), median of
     `iters` copies of an n_bytes buffer: the reference's health check method
@@ -196,6 +209,7 @@ def main(argv=None):
          f"launch avg {avg_launch_ms:.4f} ms, median {med_launch_ms:.4f} ms")
 
     copy_gbs = None if args.no_copy else copy_bandwidth(dev)
+    traffic = profiled_traffic(f"{w.name} {args.schedule} rpl={args.rpl} {args.layout} {w.store}")
     if copy_gbs:
         _log(f"[bench] device copy {copy_gbs:.0f} GB/s")
     res = {
@@ -221,7 +235,7 @@ def main(argv=None):
                    "graph": bool(args.graph),
                    "launch_ms_median": round(med_launch_ms, 5)},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS,
-                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 5), "traffic": None,
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 5), "traffic": traffic,
                      "alg_bytes_per_launch": alg_bytes,
                      "copy_gbs": round(copy_gbs, 1) if copy_gbs else None,
                      "frac_of_copy": round(achieved / copy_gbs, 5) if copy_gbs else None},
