@@ -34,7 +34,7 @@ extern "C" {
 
 /* Bumped on every struct or semantic change; the binding refuses a library
  * reporting another value. */
-#define SDFR_ABI_VERSION 2
+#define SDFR_ABI_VERSION 3
 
 /* Element types of caller arrays. */
 enum {
@@ -110,10 +110,11 @@ typedef struct SdfrPoses {
 } SdfrPoses;
 
 typedef struct SdfrImage {
-    void* out;               /* depth image, env n row-major HxW at out + n*env_stride elements */
-    int64_t env_stride;      /* elements between envs (H*W for a dense (N,H,W) tensor) */
+    void* out;               /* image of env n at out + n*env_stride elements: row-major HxW,
+                                or HxWx2 interleaved (depth, |n_z|) when channels == 2 */
+    int64_t env_stride;      /* elements between envs (H*W*channels for a dense tensor) */
     int32_t dtype;           /* SDFR_F32 or SDFR_BF16 */
-    int32_t reserved;
+    int32_t channels;        /* 1 = depth; 2 = depth + surf mask (vision.py:118-191, 558-570) */
     int32_t* taps;           /* optional per-ray census, NULL = off: grid loads issued for the ray,
                                 dense (N,H,W) int32 (tools/bench_lidar.py:45-88 counts the same loop) */
 } SdfrImage;
@@ -137,11 +138,20 @@ SDFR_API SdfrGrid* sdfr_grid_create(const SdfrGridDesc* desc, const void* src,
 
 SDFR_API void sdfr_grid_destroy(SdfrGrid* grid);
 
+/* Attaches the surf-mask grid to a handle: nz*ny*nx int8 values |n_z|*127
+ * in [nz][ny][nx] order, on exactly the SDF's grid (surfmask.py:193-201),
+ * re-laid out like the SDF copy. Needed for renders with channels == 2.
+ * Replaces the snz_flat upload of GpuLidar.__init__ (vision.py:489-497).
+ * Synchronous; 0 or < 0. */
+SDFR_API int32_t sdfr_grid_attach_surfnz(SdfrGrid* grid, const void* src, int32_t src_on_device,
+                                         void* stream);
+
 /* Chooses how sdfr_render schedules rays on this handle: `schedule` is an
  * SDFR_SCHED_* value (default SDFR_SCHED_TILES); `refill_lanes` (1..64,
  * default 16) is the number of free lanes at which a persistent wave takes
- * new rays; `rays_per_lane` (1, 2 or 4, default 2) is how many tiles a wave
- * of the tiles schedule marches at once. Results do not depend on any of them. No reference
+ * new rays; `rays_per_lane` (1 or 2, default 2) is how many tiles a wave
+ * of the tiles schedule marches at once. Surf-mask renders always use the
+ * tiles schedule. Results do not depend on any of them. No reference
  * counterpart: the Triton launch has one fixed shape (vision.py:48-54;
  * tools/proto_march.py sweeps it). */
 SDFR_API int32_t sdfr_grid_set_schedule(SdfrGrid* grid, int32_t schedule, int32_t refill_lanes,

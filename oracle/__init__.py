@@ -67,7 +67,7 @@ def _load():
     lib.oracle_march_ray.argtypes = [p, i, i, i, p, f, f, f, f, f, f, f, f, f, f, i, p]
     lib.oracle_render.restype = i
     lib.oracle_render.argtypes = [p, i, i, i, p, f, i, i, i, d, d, d, d, f, f, f, f, i,
-                                  p, p, p, p, i, p, p, i]
+                                  p, p, p, p, i, p, p, p, i]
     _lib = lib
     return lib
 
@@ -91,8 +91,11 @@ def as_stored(grid: np.ndarray, store: str) -> np.ndarray:
 def render(grid, mins, cell, origin, yaw_deg, pitch_deg, ducked, *, width=128, height=64,
            hfov_deg=120.0, vfov_deg=90.0, range_units=2000.0, near_range=None,
            hit_eps=None, min_step=None, max_steps=64, pinhole=False, store="f32",
-           threads=0):
+           surf_nz=None, threads=0):
     """Depth encodings (N,H,W) f32 and grid loads per ray (N,H,W) int32.
+
+    With ``surf_nz`` (int8 [nz,ny,nx], |n_z|*127) the image is (N,H,W,2):
+    depth and |n_z| at the voxel the march stopped in (vision.py:654-666).
 
     Defaults and derived constants follow GpuLidar (vision.py:457-509):
     near = range when not given, hit_eps = 0.6*cell, min_step = 0.3*cell
@@ -113,12 +116,18 @@ def render(grid, mins, cell, origin, yaw_deg, pitch_deg, ducked, *, width=128, h
     mstep = float(np.float32(0.3 * cell)) if min_step is None else float(min_step)
     tan_h = float(np.tan(0.5 * hfov_deg * (np.pi / 180.0)))
     tan_v = float(np.tan(0.5 * vfov_deg * (np.pi / 180.0)))
-    out = np.empty((n, height, width), np.float32)
+    nzg = None
+    if surf_nz is not None:
+        nzg = np.ascontiguousarray(surf_nz, dtype=np.int8)
+        if nzg.shape != g.shape:
+            raise ValueError(f"surf_nz grid {nzg.shape} != SDF grid {g.shape}")
+    out = np.empty((n, height, width) + ((2,) if nzg is not None else ()), np.float32)
     loads = np.empty((n, height, width), np.int32)
     rc = lib.oracle_render(_ptr(g), nx, ny, nz, _ptr(mins), float(cell), width, height,
                            1 if pinhole else 0, float(hfov_deg), float(vfov_deg), tan_h, tan_v,
                            rng, near, eps, mstep, int(max_steps), _ptr(origin), _ptr(yaw),
-                           _ptr(pitch), _ptr(duck), n, _ptr(out), _ptr(loads), int(threads))
+                           _ptr(pitch), _ptr(duck), n, _ptr(out), _ptr(loads),
+                           _ptr(nzg) if nzg is not None else None, int(threads))
     if rc != 0:
         raise ValueError("oracle_render rejected its arguments")
     return out, loads

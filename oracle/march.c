@@ -148,16 +148,20 @@ ORACLE_API float oracle_march_ray(const float* grid, int nx, int ny, int nz, con
 /* Full render of N envs into out[N][H][W] (and loads[N][H][W] if given).
  * grid holds the voxel values exactly as the renderer reads them (an f16
  * store is emulated by the caller rounding to f16 and back). Poses are
- * dense: origin[N][3], yaw/pitch/ducked[N]. Returns 0, or -1 on bad args. */
+ * dense: origin[N][3], yaw/pitch/ducked[N]. With nzg (the int8 |n_z|*127
+ * surf-mask grid, same [nz][ny][nx] shape) the output is out[N][H][W][2]:
+ * the depth encoding and |n_z| of the voxel the march stopped in, read at
+ * the clamped t (vision.py:654-666). Returns 0, or -1 on bad args. */
 ORACLE_API int oracle_render(const float* grid, int nx, int ny, int nz, const float* mins,
                              float cell, int W, int H, int camera, double hfov, double vfov,
                              double tan_h, double tan_v, float range, float near, float hit_eps,
                              float min_step, int max_steps, const float* origin, const float* yaw,
                              const float* pitch, const float* ducked, int N, float* out,
-                             int32_t* loads, int nthreads) {
+                             int32_t* loads, const int8_t* nzg, int nthreads) {
     if (!grid || !mins || !origin || !yaw || !pitch || !ducked || !out) return -1;
     if (nx <= 0 || ny <= 0 || nz <= 0 || W <= 0 || H <= 0 || N < 0 || !(near > 0.0f)) return -1;
     const float inv_cell = (float)(1.0 / (double)cell);
+    const int ch = nzg ? 2 : 1;
 #ifdef _OPENMP
     if (nthreads > 0) omp_set_num_threads(nthreads);
 #pragma omp parallel for schedule(dynamic, 1)
@@ -174,9 +178,16 @@ ORACLE_API int oracle_render(const float* grid, int nx, int ny, int nz, const fl
             float t = oracle_march_ray(grid, nx, ny, nz, mins, inv_cell, ex, ey, ez, d[0], d[1],
                                        d[2], range, hit_eps, min_step, max_steps, &nl);
             t = t < range ? t : range;
-            const size_t o = ((size_t)n * H + r) * W + c;
-            out[o] = oracle_encode(t, near);
-            if (loads) loads[o] = nl;
+            const size_t px = ((size_t)n * H + r) * W + c;
+            out[px * ch] = oracle_encode(t, near);
+            if (nzg) {
+                const int ix = clamp_index(((ex + d[0] * t) - mins[0]) * inv_cell, nx);
+                const int iy = clamp_index(((ey + d[1] * t) - mins[1]) * inv_cell, ny);
+                const int iz = clamp_index(((ez + d[2] * t) - mins[2]) * inv_cell, nz);
+                const int8_t v = nzg[((size_t)iz * (size_t)ny + (size_t)iy) * (size_t)nx + (size_t)ix];
+                out[px * ch + 1] = (float)v / 127.0f;
+            }
+            if (loads) loads[px] = nl;
         }
     }
     return 0;

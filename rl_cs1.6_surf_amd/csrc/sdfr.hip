@@ -89,7 +89,9 @@ struct SdfrGrid {
     uint32_t* counters;    // persistent schedule: tile claim counters + exit counter
     int32_t schedule;      // SDFR_SCHED_*
     int32_t refill_lanes;  // persistent schedule: refill when this many lanes are free
-    int32_t rays_per_lane; // tiles schedule: rays each lane marches at once (1, 2, 4)
+    int32_t rays_per_lane; // tiles schedule: rays each lane marches at once (1, 2)
+    void* nz_data;         // surf mask grid (int8), same layout as data, or null
+    int64_t nz_bytes;
     int device;
     int cus;               // compute units of the device
 };
@@ -214,6 +216,8 @@ struct MarchArgs {
     int nblocks;
     uint32_t* counters;           // persistent schedule only
     int refill_lanes;
+    const void* nzmask;           // surf mask: |n_z|*127 int8 copy, same layout
+    uint32_t nz_bytes;
 };
 
 // Block b runs on XCD b % 8; give XCD x the x-th contiguous eighth of the
@@ -338,7 +342,12 @@ __global__ __launch_bounds__(256) void ray_tables_kernel(MarchArgs a) {
 // The step counter is wave-uniform and the loop leaves as soon as no ray of
 // the wave is alive, which is exact: alive only turns off and a dead ray adds
 // 0 to t.
-template <typename GT, int LAYOUT, int OUT_DTYPE, int CAMERA, bool CENSUS, int RPL>
+//
+// SURF adds the surf-mask channel (vision.py:118-191): after the march the
+// voxel under the clamped depth is re-derived with the same index formula
+// and the |n_z| grid (int8, |n_z|*127) is read there; the image is then
+// interleaved (depth, |n_z|) per pixel, channel fastest (vision.py:558-570).
+template <typename GT, int LAYOUT, int OUT_DTYPE, int CAMERA, bool CENSUS, int RPL, bool SURF>
 __global__ __launch_bounds__(256) void march_tiles(MarchArgs a) {
     extern __shared__ uint32_t s_axis[];
     fill_axis_tables<GT, LAYOUT>(a, s_axis);
@@ -349,7 +358,7 @@ __global__ __launch_bounds__(256) void march_tiles(MarchArgs a) {
     if (tile0 >= a.total_tiles) return;
 
     float ex[RPL], ey[RPL], ez[RPL], dx[RPL], dy[RPL], dz[RPL], t[RPL];
-    int64_t o[RPL];
+    int env[RPL], pix[RPL];   // env index and r*W + c of each ray
     int taps[RPL];
     bool alive[RPL], valid[RPL];
 #pragma unroll
@@ -382,7 +391,8 @@ __global__ __launch_bounds__(256) void march_tiles(MarchArgs a) {
         t[j] = 0.0f;
         taps[j] = 0;
         alive[j] = valid[j];
-        o[j] = (int64_t)n * a.env_stride + (int64_t)rr * a.W + cc;
+        env[j] = n;
+        pix[j] = rr * a.W + cc;
     }
     const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<void*>(a.grid), 0, (int)a.grid_bytes, kRsrcWord3);
@@ -413,15 +423,29 @@ __global__ __launch_bounds__(256) void march_tiles(MarchArgs a) {
             }
         }
     }
+    constexpr int CH = SURF ? 2 : 1;
 #pragma unroll
     for (int j = 0; j < RPL; ++j) {
         if (valid[j]) {
-            store_enc<OUT_DTYPE>(a.out, o[j], encode_depth(fminf(t[j], a.rng), a.near));
-            if constexpr (CENSUS) {
-                const int64_t n = (o[j] - (o[j] % a.env_stride)) / a.env_stride;
-                const int64_t rc = o[j] - n * a.env_stride;
-                a.taps[n * a.H * a.W + rc] = taps[j];
+            const float tc = fminf(t[j], a.rng);
+            const int64_t o = (int64_t)env[j] * a.env_stride + (int64_t)pix[j] * CH;
+            store_enc<OUT_DTYPE>(a.out, o, encode_depth(tc, a.near));
+            if constexpr (SURF) {
+                // the voxel the march stopped in (vision.py:176-187, :658-665)
+                constexpr int kLog = sizeof(GT) == 2 ? 1 : 2;
+                const float px = ex[j] + dx[j] * tc;
+                const float py = ey[j] + dy[j] * tc;
+                const float pz = ez[j] + dz[j] * tc;
+                const int ix = (int)__builtin_amdgcn_fmed3f((px - a.mnx) * a.inv_cell, 0.0f, a.fnx1);
+                const int iy = (int)__builtin_amdgcn_fmed3f((py - a.mny) * a.inv_cell, 0.0f, a.fny1);
+                const int iz = (int)__builtin_amdgcn_fmed3f((pz - a.mnz) * a.inv_cell, 0.0f, a.fnz1);
+                const uint32_t off = (tab[ix] + tab[a.nx + iy] + tab[a.nx + a.ny + iz]) >> kLog;
+                const __amdgpu_buffer_rsrc_t nz_rsrc = __builtin_amdgcn_make_buffer_rsrc(
+                    const_cast<void*>(a.nzmask), 0, (int)a.nz_bytes, kRsrcWord3);
+                const int8_t v = (int8_t)__builtin_amdgcn_raw_buffer_load_b8(nz_rsrc, off, 0, 0);
+                store_enc<OUT_DTYPE>(a.out, o + 1, (float)v / 127.0f);
             }
+            if constexpr (CENSUS) a.taps[(int64_t)env[j] * a.H * a.W + pix[j]] = taps[j];
         }
     }
 }
@@ -606,14 +630,19 @@ __global__ __launch_bounds__(256) void relayout_grid(const ST* __restrict__ src,
         iy = by_i * 4 + ((inner >> 2) & 3);
         iz = bz_i * 4 + (inner >> 4);
     }
-    float v = 0.0f;   // padding voxels are never addressed (indices clamp to n-1)
-    if (ix < nx && iy < ny && iz < nz) {
-        const int64_t s = ((int64_t)iz * ny + iy) * nx + ix;
-        if constexpr (sizeof(ST) == 2) v = __half2float(((const __half*)src)[s]);
-        else v = ((const float*)src)[s];
+    const bool inside = ix < nx && iy < ny && iz < nz;   // padding is never addressed
+    const int64_t s = ((int64_t)iz * ny + iy) * nx + ix;
+    if constexpr (sizeof(ST) == 1) {
+        dst[i] = inside ? src[s] : (DT)0;
+    } else {
+        float v = 0.0f;
+        if (inside) {
+            if constexpr (sizeof(ST) == 2) v = __half2float(((const __half*)src)[s]);
+            else v = ((const float*)src)[s];
+        }
+        if constexpr (sizeof(DT) == 2) ((__half*)dst)[i] = __float2half_rn(v);
+        else ((float*)dst)[i] = v;
     }
-    if constexpr (sizeof(DT) == 2) ((__half*)dst)[i] = __float2half_rn(v);
-    else ((float*)dst)[i] = v;
 }
 
 template <typename ST, typename DT>
@@ -634,17 +663,28 @@ size_t axis_lds_bytes(const MarchArgs& a) {
     return sizeof(uint32_t) * (size_t)(a.nx + a.ny + a.nz);
 }
 
-template <typename GT, int LAYOUT, int OUT, int CAMERA, bool CENSUS>
-void launch_march(MarchArgs& a, const SdfrGrid* g, hipStream_t st) {
+template <typename GT, int LAYOUT, int OUT, int CAMERA, bool CENSUS, bool SURF>
+void launch_tiles(MarchArgs& a, int rpl, hipStream_t st) {
     const size_t lds = axis_lds_bytes(a);
-    if (g->schedule == SDFR_SCHED_TILES) {
-        const int rpl = g->rays_per_lane;
-        a.nblocks = (int)((a.total_tiles + 4 * rpl - 1) / (4 * rpl));
-        if (rpl == 4) march_tiles<GT, LAYOUT, OUT, CAMERA, CENSUS, 4><<<a.nblocks, 256, lds, st>>>(a);
-        else if (rpl == 2) march_tiles<GT, LAYOUT, OUT, CAMERA, CENSUS, 2><<<a.nblocks, 256, lds, st>>>(a);
-        else march_tiles<GT, LAYOUT, OUT, CAMERA, CENSUS, 1><<<a.nblocks, 256, lds, st>>>(a);
+    a.nblocks = (int)((a.total_tiles + 4 * rpl - 1) / (4 * rpl));
+    if (rpl == 2) march_tiles<GT, LAYOUT, OUT, CAMERA, CENSUS, 2, SURF><<<a.nblocks, 256, lds, st>>>(a);
+    else march_tiles<GT, LAYOUT, OUT, CAMERA, CENSUS, 1, SURF><<<a.nblocks, 256, lds, st>>>(a);
+}
+
+template <typename GT, int LAYOUT, int OUT, int CAMERA, bool CENSUS>
+void launch_march(MarchArgs& a, const SdfrGrid* g, bool surf, hipStream_t st) {
+    if (surf) {
+        // the surf-mask variant exists for the equiangular camera only
+        // (vision.py:463-467) and always runs the tiles schedule
+        if constexpr (CAMERA == SDFR_CAM_EQUIANGULAR)
+            launch_tiles<GT, LAYOUT, OUT, CAMERA, CENSUS, true>(a, g->rays_per_lane, st);
         return;
     }
+    if (g->schedule == SDFR_SCHED_TILES) {
+        launch_tiles<GT, LAYOUT, OUT, CAMERA, CENSUS, false>(a, g->rays_per_lane, st);
+        return;
+    }
+    const size_t lds = axis_lds_bytes(a);
     // a grid that fills every CU once, never more blocks than the tiles need
     int per_cu = 0;
     if (hipOccupancyMaxActiveBlocksPerMultiprocessor(
@@ -658,20 +698,21 @@ void launch_march(MarchArgs& a, const SdfrGrid* g, hipStream_t st) {
 }
 
 template <typename GT, int LAYOUT, int OUT>
-void dispatch_cam(MarchArgs& a, const SdfrGrid* g, bool census, hipStream_t st) {
+void dispatch_cam(MarchArgs& a, const SdfrGrid* g, bool census, bool surf, hipStream_t st) {
     if (a.camera == SDFR_CAM_PINHOLE) {
-        if (census) launch_march<GT, LAYOUT, OUT, SDFR_CAM_PINHOLE, true>(a, g, st);
-        else launch_march<GT, LAYOUT, OUT, SDFR_CAM_PINHOLE, false>(a, g, st);
+        if (census) launch_march<GT, LAYOUT, OUT, SDFR_CAM_PINHOLE, true>(a, g, surf, st);
+        else launch_march<GT, LAYOUT, OUT, SDFR_CAM_PINHOLE, false>(a, g, surf, st);
     } else {
-        if (census) launch_march<GT, LAYOUT, OUT, SDFR_CAM_EQUIANGULAR, true>(a, g, st);
-        else launch_march<GT, LAYOUT, OUT, SDFR_CAM_EQUIANGULAR, false>(a, g, st);
+        if (census) launch_march<GT, LAYOUT, OUT, SDFR_CAM_EQUIANGULAR, true>(a, g, surf, st);
+        else launch_march<GT, LAYOUT, OUT, SDFR_CAM_EQUIANGULAR, false>(a, g, surf, st);
     }
 }
 
 template <typename GT, int LAYOUT>
-void dispatch_out(MarchArgs& a, const SdfrGrid* g, int out_dtype, bool census, hipStream_t st) {
-    if (out_dtype == SDFR_BF16) dispatch_cam<GT, LAYOUT, SDFR_BF16>(a, g, census, st);
-    else dispatch_cam<GT, LAYOUT, SDFR_F32>(a, g, census, st);
+void dispatch_out(MarchArgs& a, const SdfrGrid* g, int out_dtype, bool census, bool surf,
+                  hipStream_t st) {
+    if (out_dtype == SDFR_BF16) dispatch_cam<GT, LAYOUT, SDFR_BF16>(a, g, census, surf, st);
+    else dispatch_cam<GT, LAYOUT, SDFR_F32>(a, g, census, surf, st);
 }
 
 bool dtype_ok_for_ducked(int d) {
@@ -825,6 +866,8 @@ SDFR_API SdfrGrid* sdfr_grid_create(const SdfrGridDesc* desc, const void* src, i
     g->bytes = count * elem;
     g->data = nullptr;
     g->counters = nullptr;
+    g->nz_data = nullptr;
+    g->nz_bytes = 0;
     g->schedule = SDFR_SCHED_TILES;
     g->refill_lanes = 16;
     g->rays_per_lane = 2;
@@ -871,8 +914,40 @@ SDFR_API SdfrGrid* sdfr_grid_create(const SdfrGridDesc* desc, const void* src, i
 SDFR_API void sdfr_grid_destroy(SdfrGrid* grid) {
     if (!grid) return;
     if (grid->data) (void)hipFree(grid->data);
+    if (grid->nz_data) (void)hipFree(grid->nz_data);
     if (grid->counters) (void)hipFree(grid->counters);
     delete grid;
+}
+
+SDFR_API int32_t sdfr_grid_attach_surfnz(SdfrGrid* grid, const void* src, int32_t src_on_device,
+                                         void* stream) {
+    g_err[0] = '\0';
+    if (!grid || !grid->data) return fail(-1, "sdfr_grid_attach_surfnz: null grid handle");
+    if (!src) return fail(-1, "sdfr_grid_attach_surfnz: null source");
+    hipStream_t st = (hipStream_t)stream;
+    const int64_t nvox = (int64_t)grid->desc.nx * grid->desc.ny * grid->desc.nz;
+    const int64_t count = grid->layout == SDFR_LAYOUT_BRICK4
+                              ? (int64_t)grid->bx * grid->by * grid->bz * 64 : nvox;
+    void* dst = nullptr;
+    void* staged = nullptr;
+    const void* dsrc = src;
+    hipError_t e = hipMalloc(&dst, (size_t)count);
+    if (e == hipSuccess && !src_on_device) {
+        e = hipMalloc(&staged, (size_t)nvox);
+        if (e == hipSuccess) e = hipMemcpyAsync(staged, src, (size_t)nvox, hipMemcpyHostToDevice, st);
+        dsrc = staged;
+    }
+    if (e == hipSuccess) e = launch_relayout<int8_t, int8_t>(dsrc, dst, grid, count, st);
+    if (e == hipSuccess) e = hipStreamSynchronize(st);
+    if (staged) (void)hipFree(staged);
+    if (e != hipSuccess) {
+        if (dst) (void)hipFree(dst);
+        return fail(-4, "sdfr_grid_attach_surfnz: HIP error %s", hipGetErrorString(e));
+    }
+    if (grid->nz_data) (void)hipFree(grid->nz_data);
+    grid->nz_data = dst;
+    grid->nz_bytes = count;
+    return 0;
 }
 
 SDFR_API int32_t sdfr_grid_set_schedule(SdfrGrid* grid, int32_t schedule, int32_t refill_lanes,
@@ -884,8 +959,8 @@ SDFR_API int32_t sdfr_grid_set_schedule(SdfrGrid* grid, int32_t schedule, int32_
     if (refill_lanes < 1 || refill_lanes > 64)
         return fail(-2, "sdfr_grid_set_schedule: refill_lanes must be in 1..64 (got %d)",
                     refill_lanes);
-    if (rays_per_lane != 1 && rays_per_lane != 2 && rays_per_lane != 4)
-        return fail(-2, "sdfr_grid_set_schedule: rays_per_lane must be 1, 2 or 4 (got %d)",
+    if (rays_per_lane != 1 && rays_per_lane != 2)
+        return fail(-2, "sdfr_grid_set_schedule: rays_per_lane must be 1 or 2 (got %d)",
                     rays_per_lane);
     grid->schedule = schedule;
     grid->refill_lanes = refill_lanes;
@@ -904,8 +979,15 @@ SDFR_API int32_t sdfr_render(const SdfrGrid* grid, const SdfrCam* cam, const Sdf
     if (!image->out) return fail(-1, "sdfr_render: null output pointer");
     if (image->dtype != SDFR_F32 && image->dtype != SDFR_BF16)
         return fail(-3, "sdfr_render: output dtype must be f32 or bf16 (got %d)", image->dtype);
-    if (image->env_stride < (int64_t)cam->width * cam->height)
-        return fail(-2, "sdfr_render: env_stride %lld is smaller than H*W",
+    if (image->channels != 1 && image->channels != 2)
+        return fail(-3, "sdfr_render: channels must be 1 or 2 (got %d)", image->channels);
+    const bool surf = image->channels == 2;
+    if (surf && !grid->nz_data)
+        return fail(-1, "sdfr_render: 2 channels need a surf-mask grid (sdfr_grid_attach_surfnz)");
+    if (surf && cam->camera != SDFR_CAM_EQUIANGULAR)
+        return fail(-3, "sdfr_render: the surf-mask channel has no pinhole kernel");
+    if (image->env_stride < (int64_t)cam->width * cam->height * image->channels)
+        return fail(-2, "sdfr_render: env_stride %lld is smaller than H*W*channels",
                     (long long)image->env_stride);
     const int64_t need = workspace_bytes(cam->width, cam->height, poses->n_envs);
     if (!workspace || workspace_size < need)
@@ -937,6 +1019,8 @@ SDFR_API int32_t sdfr_render(const SdfrGrid* grid, const SdfrCam* cam, const Sdf
     a.taps = image->taps;
     a.counters = grid->counters;
     a.refill_lanes = grid->refill_lanes;
+    a.nzmask = grid->nz_data;
+    a.nz_bytes = (uint32_t)grid->nz_bytes;
     a.tiles_x = (cam->width + 7) / 8;
     a.tiles_per_env = a.tiles_x * ((cam->height + 7) / 8);
     a.total_tiles = (int64_t)a.tiles_per_env * poses->n_envs;
@@ -951,14 +1035,14 @@ SDFR_API int32_t sdfr_render(const SdfrGrid* grid, const SdfrCam* cam, const Sdf
     const bool census = image->taps != nullptr;
     if (grid->store_dtype == SDFR_F16) {
         if (grid->layout == SDFR_LAYOUT_BRICK4)
-            dispatch_out<__half, SDFR_LAYOUT_BRICK4>(a, grid, image->dtype, census, st);
+            dispatch_out<__half, SDFR_LAYOUT_BRICK4>(a, grid, image->dtype, census, surf, st);
         else
-            dispatch_out<__half, SDFR_LAYOUT_LINEAR>(a, grid, image->dtype, census, st);
+            dispatch_out<__half, SDFR_LAYOUT_LINEAR>(a, grid, image->dtype, census, surf, st);
     } else {
         if (grid->layout == SDFR_LAYOUT_BRICK4)
-            dispatch_out<float, SDFR_LAYOUT_BRICK4>(a, grid, image->dtype, census, st);
+            dispatch_out<float, SDFR_LAYOUT_BRICK4>(a, grid, image->dtype, census, surf, st);
         else
-            dispatch_out<float, SDFR_LAYOUT_LINEAR>(a, grid, image->dtype, census, st);
+            dispatch_out<float, SDFR_LAYOUT_LINEAR>(a, grid, image->dtype, census, surf, st);
     }
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return fail(-4, "sdfr_render: launch failed: %s", hipGetErrorString(e));

@@ -18,7 +18,7 @@ import torch  # noqa: F401  (load torch's HIP runtime first, see above)
 PKG_ROOT = Path(__file__).resolve().parents[1]
 LIB_PATH = PKG_ROOT / "lib" / "libsdfr.so"
 
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 # element types (SDFR_* in sdfr.h)
 F32, F16, BF16, I32, I64, U8, F64 = 0, 1, 2, 3, 4, 5, 6
@@ -27,8 +27,8 @@ CAM_EQUIANGULAR, CAM_PINHOLE = 0, 1
 SCHED_PERSISTENT, SCHED_TILES = 0, 1
 
 EXPORTS = ("sdfr_abi_version", "sdfr_last_error", "sdfr_grid_create", "sdfr_grid_destroy",
-           "sdfr_grid_bytes", "sdfr_grid_set_schedule", "sdfr_workspace_bytes", "sdfr_render",
-           "sdfr_ray_dirs")
+           "sdfr_grid_bytes", "sdfr_grid_attach_surfnz", "sdfr_grid_set_schedule",
+           "sdfr_workspace_bytes", "sdfr_render", "sdfr_ray_dirs")
 
 
 class GridDesc(ctypes.Structure):
@@ -55,7 +55,7 @@ class Poses(ctypes.Structure):
 
 class Image(ctypes.Structure):
     _fields_ = [("out", ctypes.c_void_p), ("env_stride", ctypes.c_int64),
-                ("dtype", ctypes.c_int32), ("reserved", ctypes.c_int32),
+                ("dtype", ctypes.c_int32), ("channels", ctypes.c_int32),
                 ("taps", ctypes.c_void_p)]
 
 
@@ -88,6 +88,8 @@ def load(path: Path | str | None = None):
     lib.sdfr_grid_destroy.argtypes = [vp]
     lib.sdfr_grid_bytes.restype = i64
     lib.sdfr_grid_bytes.argtypes = [vp]
+    lib.sdfr_grid_attach_surfnz.restype = i32
+    lib.sdfr_grid_attach_surfnz.argtypes = [vp, vp, i32, vp]
     lib.sdfr_grid_set_schedule.restype = i32
     lib.sdfr_grid_set_schedule.argtypes = [vp, i32, i32, i32]
     lib.sdfr_workspace_bytes.restype = i64

@@ -129,13 +129,12 @@ class GpuLidar:
                  pinhole: bool = False, *, grid_dtype=torch.float16,
                  layout: str = "brick4", hit_eps: float = None,
                  min_step: float = None, schedule: str = "tiles",
-                 refill_lanes: int = 16, rays_per_lane: int = 2, _grid=None) -> None:
+                 refill_lanes: int = 16, rays_per_lane: int = 2, _grid=None,
+                 _surf_nz=None) -> None:
         if surf_mask and pinhole:
             raise ValueError(
                 "surf_mask and pinhole are separate experiments and there is "
                 "no combined kernel")
-        if surf_mask:
-            raise NotImplementedError("the |n_z| surf-mask channel is not built in this renderer")
         self.device = torch.device(device)
         if self.device.type != "cuda":
             raise ValueError(f"GpuLidar renders on a ROCm GPU (device='cuda'), got {device!r}; "
@@ -162,8 +161,24 @@ class GpuLidar:
         self.mins = torch.as_tensor(mins, device=self.device)
         self.mins_f = (float(mins[0]), float(mins[1]), float(mins[2]))
         self.cell = float(cell)
-        self.surf_mask = False
-        self.channels = 1
+        # second channel: |n_z| of the hit surface (vision.py:482-497), on
+        # exactly the SDF's voxels; nothing is allocated for it when off
+        self.surf_mask = bool(surf_mask)
+        self.channels = 2 if self.surf_mask else 1
+        snz = None
+        if self.surf_mask:
+            if _surf_nz is not None:
+                snz = np.asarray(_surf_nz)
+            else:
+                from . import surfmask
+                snz, _ = surfmask.build_surfnz(core, cell)
+                snz = np.asarray(snz)
+            if snz.shape != sdf.shape:
+                raise RuntimeError(
+                    f"surfability grid {snz.shape} != SDF grid {sdf.shape}: "
+                    "the march reads both with ONE voxel index")
+            self.snz_flat = torch.as_tensor(snz.astype(np.int8, copy=False),
+                                            device=self.device).reshape(-1)
         self.W, self.H = int(width), int(height)
         self.range = float(range_units)
         self.near = float(near_range) if near_range else self.range
@@ -204,6 +219,11 @@ class GpuLidar:
         if not h:
             raise _sdfr.SdfrError(err.value.decode("utf-8", "replace"))
         self._grid = h
+        if self.surf_mask:
+            with torch.cuda.device(self.device):
+                stream = torch.cuda.current_stream(self.device).cuda_stream
+                rc = self._lib.sdfr_grid_attach_surfnz(h, self.snz_flat.data_ptr(), 1, stream)
+            _sdfr.check(rc, "sdfr_grid_attach_surfnz", self._lib)
         self.set_schedule(schedule, refill_lanes, rays_per_lane)
 
     def set_schedule(self, schedule: str = "tiles", refill_lanes: int = 16,
@@ -218,11 +238,15 @@ class GpuLidar:
         self.rays_per_lane = int(rays_per_lane)
 
     @classmethod
-    def from_grid(cls, sdf, mins, cell, **kwargs) -> "GpuLidar":
-        """A lidar over an explicit [nz,ny,nx] distance grid (no map core)."""
+    def from_grid(cls, sdf, mins, cell, surf_nz=None, **kwargs) -> "GpuLidar":
+        """A lidar over an explicit [nz,ny,nx] distance grid (no map core);
+        ``surf_nz`` (int8 |n_z|*127 on the same grid) enables the second
+        channel."""
         kwargs = dict(kwargs)
         kwargs["cell"] = float(cell)
-        return cls(None, _grid=(sdf, mins, float(cell)), **kwargs)
+        if surf_nz is not None:
+            kwargs["surf_mask"] = True
+        return cls(None, _grid=(sdf, mins, float(cell)), _surf_nz=surf_nz, **kwargs)
 
     def __del__(self):
         h = getattr(self, "_grid", None)
@@ -287,8 +311,9 @@ class GpuLidar:
     def _check_out(self, out: torch.Tensor, n: int) -> int:
         if out.device != self.device or out.dtype not in _OUT_DTYPES:
             raise ValueError("out must be a float32 or bfloat16 tensor on the lidar's device")
-        if out.shape[0] != n or out[0].numel() != self.H * self.W:
-            raise ValueError(f"out must hold N={n} images of {self.H}x{self.W}, "
+        per_env = self.H * self.W * self.channels
+        if out.shape[0] != n or out[0].numel() != per_env:
+            raise ValueError(f"out must hold N={n} images of {self.H}x{self.W}x{self.channels}, "
                              f"got {tuple(out.shape)}")
         # each env's image must be one dense row-major HxW block
         inner = out[0]
@@ -297,13 +322,14 @@ class GpuLidar:
             if size != 1 and stride != expect:
                 raise ValueError("each env's image in out must be contiguous")
             expect *= size
-        return out.stride(0) if n > 1 else self.H * self.W
+        return out.stride(0) if n > 1 else per_env
 
     # ---------------------------------------------------------------- render --
     @torch.no_grad()
     def render(self, origin, yaw_deg, pitch_deg, ducked, out=None, taps=None):
         """origin (N,3), yaw/pitch (N,) degrees, ducked (N,) bool/int/float ->
-        (N, H, W) float32 depth encodings (vision.py:542-550).
+        (N, H, W) float32 depth encodings, or (N, H, W, 2) (depth, |n_z|)
+        channel-fastest with the surf mask (vision.py:542-550).
 
         Inputs may be strided views (the trainer passes columns of its (N,6)
         pose tensor). ``out`` optionally names the destination — any float32
@@ -314,7 +340,8 @@ class GpuLidar:
         poses, keep = self._poses(origin, yaw_deg, pitch_deg, ducked)
         n = poses.n_envs
         if out is None:
-            out = torch.empty(n, self.H, self.W, device=self.device)
+            shape = (n, self.H, self.W, 2) if self.surf_mask else (n, self.H, self.W)
+            out = torch.empty(shape, device=self.device)
         env_stride = self._check_out(out, n)
         taps_ptr = None
         if taps is not None:
@@ -322,7 +349,8 @@ class GpuLidar:
                     or taps.numel() != n * self.H * self.W):
                 raise ValueError("taps must be a contiguous int32 (N,H,W) tensor on the device")
             taps_ptr = taps.data_ptr()
-        img = _sdfr.Image(out.data_ptr(), env_stride, _OUT_DTYPES[out.dtype], 0, taps_ptr)
+        img = _sdfr.Image(out.data_ptr(), env_stride, _OUT_DTYPES[out.dtype], self.channels,
+                          taps_ptr)
         cam = self._cam()
         ws = self._workspace(cam, n)
         with torch.cuda.device(self.device):

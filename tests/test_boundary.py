@@ -99,7 +99,7 @@ def test_grid_create_rejects_bad_descriptors_without_a_device():
 def test_render_rejects_bad_arguments_without_a_device():
     from surfgym import _sdfr
     lib = _sdfr.load()
-    img = _sdfr.Image(64, 128 * 64, _sdfr.F32, 0, None)
+    img = _sdfr.Image(64, 128 * 64, _sdfr.F32, 1, None)
     rc = lib.sdfr_render(None, ctypes.byref(_cam()), ctypes.byref(_poses()), ctypes.byref(img),
                          None, 0, None)
     assert rc == -1 and "grid" in _sdfr.last_error()
@@ -131,6 +131,9 @@ def test_lidar_refuses_the_cpu_instead_of_falling_back():
                                   device="cpu")
     with pytest.raises(ValueError, match="no combined kernel"):
         vision.GpuLidar(None, surf_mask=True, pinhole=True)
+    with pytest.raises(ValueError, match="no CPU path"):
+        vision.GpuLidar.from_grid(np.full((4, 4, 4), 99.0, np.float32), np.zeros(3), 16.0,
+                                  surf_nz=np.zeros((4, 4, 4), np.int8), device="cpu")
 
 
 def test_missing_library_is_an_error(tmp_path):

@@ -233,7 +233,7 @@ def test_ragged_images_match_the_oracle(dev, W, H, n):
     assert (np.abs(got - want) <= ENC_TOL).mean() >= 0.99
 
 
-@pytest.mark.parametrize("refill,rpl", [(1, 1), (16, 2), (48, 4), (64, 1)])
+@pytest.mark.parametrize("refill,rpl", [(1, 1), (16, 2), (48, 2), (64, 1)])
 def test_schedules_give_identical_results(dev, refill, rpl):
     """Persistent waves with ray refill and one-wave-per-tile launches march
     the same rays: outputs and censuses must be bit-identical, whatever the
