@@ -105,6 +105,47 @@ def copy_bandwidth(dev, n_bytes=2_000_000_000, iters=10):
     return 2 * n_bytes / (statistics.median(ms) * 1e-3) / 1e9
 
 
+def bench_bake(args, w, dev):
+    """SDF bake: the workload's solid occupancy through sdf_from_occupancy
+    (HIP events, median of the timed runs) and through the reference's scipy
+    call on this host (one run)."""
+    import numpy as np
+    import torch
+    from surfgym import vision
+    sc = w.scene()
+    occ = (sc.sdf == 0).astype(np.uint8)
+    occ_dev = torch.as_tensor(occ, device=dev)
+    for _ in range(max(1, args.warmup)):
+        vision.sdf_from_occupancy(occ_dev, sc.cell, device=dev)
+    torch.cuda.synchronize()
+    ms = []
+    for _ in range(args.steps):
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record()
+        vision.sdf_from_occupancy(occ_dev, sc.cell, device=dev)
+        e1.record()
+        torch.cuda.synchronize()
+        ms.append(e0.elapsed_time(e1))
+    gpu_ms = statistics.median(ms)
+    res = {"metric": "SDF bake ms (exact EDT of the occupancy)", "value": round(gpu_ms, 4),
+           "unit": "ms", "higher_is_better": False, "n_gpus": 1, "steps": args.steps,
+           "warmup": args.warmup, "data": "synthetic",
+           "config": {"workload": w.name, "grid": f"{sc.nx}x{sc.ny}x{sc.nz}",
+                      "voxels": int(occ.size), "cell": sc.cell},
+           "cpu_baseline": None}
+    if not args.no_cpu:
+        from oracle import edt
+        t0 = time.perf_counter()
+        edt.stored(edt.bake(occ, sc.cell))
+        cpu_s = time.perf_counter() - t0
+        res["cpu_baseline"] = {"value": round(cpu_s * 1e3, 1), "unit": "ms", "cores": 1,
+                               "kind": "reference",
+                               "sample": "scipy.ndimage.distance_transform_edt on the padded "
+                                         "occupancy, the reference's own bake call, one run"}
+    print(json.dumps(res), flush=True)
+
+
 def main(argv=None):
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -115,9 +156,13 @@ def main(argv=None):
     ap.add_argument("--schedule", default="tiles", choices=["persistent", "tiles"])
     ap.add_argument("--refill", type=int, default=16, help="free lanes that trigger a refill")
     ap.add_argument("--rpl", type=int, default=2, help="tiles schedule: rays per lane (1, 2, 4)")
-    ap.add_argument("--cpu-envs", type=int, default=512)
+    ap.add_argument("--cpu-envs", type=int, default=2048,
+                    help="envs of the workload the CPU baseline renders (default: all of ramp_field)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-copy", action="store_true", help="skip the copy-bandwidth probe")
+    ap.add_argument("--bake", action="store_true",
+                    help="time the SDF bake (GPU distance transform of the workload's "
+                         "occupancy) against the reference's scipy bake instead")
     ap.add_argument("--graph", action="store_true",
                     help="capture one render in a hipGraph and time graph replays")
     args = ap.parse_args(argv)
@@ -132,6 +177,8 @@ def main(argv=None):
 
     w = synth.WORKLOADS[args.workload]
     dev = torch.device("cuda:0")
+    if args.bake:
+        return bench_bake(args, w, dev)
     t0 = time.perf_counter()
     sc = w.scene()
     ps = w.poses(sc)

@@ -186,6 +186,22 @@ SDFR_API int32_t sdfr_render(const SdfrGrid* grid, const SdfrCam* cam,
 SDFR_API int32_t sdfr_ray_dirs(const SdfrCam* cam, const SdfrPoses* poses, float* dirs,
                                void* stream);
 
+/* ---- SDF bake ------------------------------------------------------------
+ * Exact Euclidean distance transform of an occupancy grid: what the
+ * reference's build_sdf computes with scipy (vision.py:428-438): pad one
+ * layer of solid around the grid, distance_transform_edt(occ == 0,
+ * sampling=cell), crop. `occ` is nz*ny*nx bytes in [nz][ny][nx] order on the
+ * device (nonzero = solid); `out` receives nz*ny*nx distances in map units
+ * (SDFR_F32 or SDFR_F16, rounded once from fp64), 0 in solid voxels.
+ * Bit-identical to the reference's bake for power-of-two cells.
+ * `workspace`: sdfr_edt_workspace_bytes() bytes of device memory, 4-byte
+ * aligned. Asynchronous on `stream`; 0 or < 0 (sdfr_edt_last_error()). */
+SDFR_API int64_t sdfr_edt_workspace_bytes(int32_t nx, int32_t ny, int32_t nz);
+SDFR_API int32_t sdfr_edt(const uint8_t* occ, int32_t nx, int32_t ny, int32_t nz, float cell,
+                          void* out, int32_t out_dtype, void* workspace, int64_t workspace_size,
+                          void* stream);
+SDFR_API const char* sdfr_edt_last_error(void);
+
 /* Message of the calling thread's most recent error ("" if none). */
 SDFR_API const char* sdfr_last_error(void);
 

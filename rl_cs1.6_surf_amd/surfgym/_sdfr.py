@@ -28,7 +28,8 @@ SCHED_PERSISTENT, SCHED_TILES = 0, 1
 
 EXPORTS = ("sdfr_abi_version", "sdfr_last_error", "sdfr_grid_create", "sdfr_grid_destroy",
            "sdfr_grid_bytes", "sdfr_grid_attach_surfnz", "sdfr_grid_set_schedule",
-           "sdfr_workspace_bytes", "sdfr_render", "sdfr_ray_dirs")
+           "sdfr_workspace_bytes", "sdfr_render", "sdfr_ray_dirs", "sdfr_edt_workspace_bytes",
+           "sdfr_edt", "sdfr_edt_last_error")
 
 
 class GridDesc(ctypes.Structure):
@@ -99,6 +100,12 @@ def load(path: Path | str | None = None):
                                 ctypes.POINTER(Image), vp, i64, vp]
     lib.sdfr_ray_dirs.restype = i32
     lib.sdfr_ray_dirs.argtypes = [ctypes.POINTER(Cam), ctypes.POINTER(Poses), vp, vp]
+    lib.sdfr_edt_workspace_bytes.restype = i64
+    lib.sdfr_edt_workspace_bytes.argtypes = [i32, i32, i32]
+    lib.sdfr_edt.restype = i32
+    lib.sdfr_edt.argtypes = [vp, i32, i32, i32, ctypes.c_float, vp, i32, vp, i64, vp]
+    lib.sdfr_edt_last_error.restype = ctypes.c_char_p
+    lib.sdfr_edt_last_error.argtypes = []
     got = lib.sdfr_abi_version()
     if got != ABI_VERSION:
         raise SdfrError(f"{p} reports ABI {got}, this binding mirrors ABI {ABI_VERSION}: "

@@ -27,7 +27,8 @@ import torch
 
 from . import _sdfr
 
-__all__ = ["GpuLidar", "build_sdf", "pick_cell", "grid_dims", "SOLID_ENT_CLASSES"]
+__all__ = ["GpuLidar", "build_sdf", "sdf_from_occupancy", "pick_cell", "grid_dims",
+           "SOLID_ENT_CLASSES"]
 
 # brush entities the reference's physics collides with (vision.py:301-307);
 # kept for importers of the name, the bake itself is not part of this module
@@ -93,6 +94,45 @@ def build_sdf(core, cell: float = 16.0, cache_dir=None):
     raise FileNotFoundError(
         f"no current SDF bake at {f} (signature {sig}); bake it once with the "
         "reference's build_sdf, or pass a grid to GpuLidar.from_grid")
+
+
+@torch.no_grad()
+def sdf_from_occupancy(occ, cell: float, device="cuda", dtype=None) -> torch.Tensor:
+    """The SDF bake on the GPU: exact Euclidean distance (map units) from
+    every voxel centre to the nearest solid voxel centre, the grid padded with
+    one layer of solid — what build_sdf computes with
+    ``scipy.ndimage.distance_transform_edt`` (vision.py:428-438), bit for bit
+    for power-of-two cells.
+
+    ``occ``: [nz, ny, nx] solid occupancy (nonzero = solid), numpy or torch.
+    ``dtype``: torch.float32 / torch.float16; None picks the reference's rule
+    (float16 above 100 M voxels, vision.py:436-437). Returns a device tensor.
+    """
+    lib = _sdfr.load()
+    device = torch.device(device)
+    if device.type != "cuda":
+        raise ValueError("the SDF bake runs on a ROCm GPU")
+    o = torch.as_tensor(np.asarray(occ) if not torch.is_tensor(occ) else occ)
+    if o.dim() != 3:
+        raise ValueError(f"occupancy must be [nz, ny, nx], got shape {tuple(o.shape)}")
+    o = (o != 0).to(device=device, dtype=torch.uint8).contiguous()
+    nz, ny, nx = (int(v) for v in o.shape)
+    if dtype is None:
+        dtype = torch.float16 if o.numel() > 100e6 else torch.float32
+    if dtype not in (torch.float32, torch.float16):
+        raise ValueError("dtype must be torch.float32 or torch.float16")
+    need = int(lib.sdfr_edt_workspace_bytes(nx, ny, nz))
+    ws = torch.empty(need, dtype=torch.uint8, device=device)
+    out = torch.empty(nz, ny, nx, dtype=dtype, device=device)
+    with torch.cuda.device(device):
+        stream = torch.cuda.current_stream(device).cuda_stream
+        rc = lib.sdfr_edt(o.data_ptr(), nx, ny, nz, float(cell), out.data_ptr(),
+                          _sdfr.F32 if dtype == torch.float32 else _sdfr.F16, ws.data_ptr(),
+                          need, stream)
+    if rc != 0:
+        raise _sdfr.SdfrError(f"sdfr_edt failed ({rc}): "
+                              f"{lib.sdfr_edt_last_error().decode('utf-8', 'replace')}")
+    return out
 
 
 def _ducked_code(t: torch.Tensor) -> int:

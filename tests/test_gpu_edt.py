@@ -1,0 +1,55 @@
+"""The on-device SDF bake (sdfr_edt) against the reference's bake, i.e.
+scipy.ndimage.distance_transform_edt on the solid-padded occupancy
+(python/surfgym/vision.py:428-438; oracle/edt.py), bit for bit."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import edt
+from surfgym import synth, vision
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.mark.parametrize("seed", range(6))
+def test_random_occupancy_matches_scipy(dev, seed):
+    rng = np.random.default_rng(100 + seed)
+    shp = tuple(int(v) for v in rng.integers(1, 70, 3))
+    occ = (rng.random(shp) < rng.uniform(0.0, 0.2)).astype(np.uint8)
+    cell = (16.0, 32.0, 8.0)[seed % 3]
+    print(f"case edt random shape={shp} cell={cell}", flush=True)
+    ref = edt.bake(occ, cell)
+    got = vision.sdf_from_occupancy(occ, cell, device=dev, dtype=torch.float32).cpu().numpy()
+    assert np.array_equal(got, ref.astype(np.float32))
+    got16 = vision.sdf_from_occupancy(occ, cell, device=dev, dtype=torch.float16).cpu().numpy()
+    assert np.array_equal(got16, ref.astype(np.float16))
+
+
+def test_empty_and_full_grids(dev):
+    print("case edt empty/full", flush=True)
+    for occ in (np.zeros((5, 7, 9), np.uint8), np.ones((5, 7, 9), np.uint8),
+                np.zeros((1, 1, 1), np.uint8), np.zeros((40, 1, 3), np.uint8)):
+        ref = edt.bake(occ, 16.0)
+        got = vision.sdf_from_occupancy(occ, 16.0, device=dev).cpu().numpy()
+        assert np.array_equal(got, ref.astype(np.float32)), occ.shape
+
+
+def test_scene_occupancy_matches_scipy_and_renders(dev):
+    """The ramp_field scene's solids (256x256x128, 8.4 M voxels): baked on the
+    GPU, equal to scipy's bake, and renderable as is."""
+    w = synth.WORKLOADS["ramp_field"]
+    sc = w.scene()
+    occ = (sc.sdf == 0).astype(np.uint8)
+    print(f"case edt ramp_field {occ.shape}", flush=True)
+    got = vision.sdf_from_occupancy(occ, sc.cell, device=dev)
+    ref = edt.stored(edt.bake(occ, sc.cell))
+    assert got.dtype == torch.float32
+    assert np.array_equal(got.cpu().numpy(), ref)
+    lid = vision.GpuLidar.from_grid(got.cpu().numpy(), sc.mins, sc.cell, grid_dtype=torch.float32,
+                                    device=dev)
+    ps = w.poses(sc, 4)
+    img = lid.render(torch.as_tensor(ps.origin, device=dev), torch.as_tensor(ps.yaw, device=dev),
+                     torch.as_tensor(ps.pitch, device=dev), torch.as_tensor(ps.ducked, device=dev))
+    assert torch.isfinite(img).all() and img.min() >= 0

@@ -279,3 +279,23 @@ def test_march_invariants_on_a_ramp_scene():
         # the stop sample is within one fp32 rounding of p: it reads <= eps
         assert sc.grid_value(p[None])[0] <= w.hit_eps + 1e-6 or \
             sc.grid_value((p + d * 1e-2)[None])[0] <= w.hit_eps
+
+
+# ------------------------------------------------------------------ SDF bake --
+def test_bake_matches_brute_force_on_tiny_grids():
+    """oracle.edt.bake is the reference's scipy call (vision.py:428-432); an
+    exhaustive nearest-solid search pins it, padding shell included."""
+    from oracle import edt
+    rng = np.random.default_rng(3)
+    for trial in range(12):
+        shp = tuple(int(v) for v in rng.integers(1, 9, 3))
+        occ = (rng.random(shp) < rng.uniform(0.0, 0.25)).astype(np.uint8)
+        cell = (16.0, 32.0, 8.0)[trial % 3]
+        assert np.allclose(edt.bake(occ, cell), edt.brute_force(occ, cell), rtol=0, atol=1e-9)
+    # closed forms: an empty grid measures the distance to the padding shell
+    occ = np.zeros((3, 4, 5), np.uint8)
+    d = edt.bake(occ, 16.0)
+    z, y, x = np.indices(occ.shape)
+    shell = np.minimum.reduce([x + 1, 5 - x, y + 1, 4 - y, z + 1, 3 - z]) * 16.0
+    assert np.array_equal(d, shell)
+    assert edt.stored(d).dtype == np.float32
