@@ -146,6 +146,130 @@ def bench_bake(args, w, dev):
     print(json.dumps(res), flush=True)
 
 
+def _reference_goal_sweeps_torch(occ_dev, cell, lo, hi):
+    """The reference's goal-field bake loop (goalfield.py:232-270) as torch
+    ops on this GPU: 26 shifted add+minimum passes per sweep over the whole
+    grid, solids re-pinned each sweep, a float64 convergence probe every 64
+    sweeps, at most 8000 sweeps. Returns (sweeps, seconds). A comparator for
+    the bake's speed, not a checker."""
+    import numpy as np
+    import torch
+    dev = occ_dev.device
+    solid = occ_dev != 0
+    nz, ny, nx = solid.shape
+    inf = float("inf")
+    dpad = torch.full((nz + 2, ny + 2, nx + 2), inf, device=dev)
+    d = torch.full((nz, ny, nx), inf, device=dev)
+    seed = torch.zeros_like(solid)
+    seed[lo[2]:hi[2] + 1, lo[1]:hi[1] + 1, lo[0]:hi[0] + 1] = True
+    seed &= ~solid
+    d[seed] = 0.0
+    del seed
+    offs = [(oz, oy, ox) for oz in (-1, 0, 1) for oy in (-1, 0, 1) for ox in (-1, 0, 1)
+            if (oz, oy, ox) != (0, 0, 0)]
+    wts = [cell * float(np.sqrt(oz * oz + oy * oy + ox * ox)) for oz, oy, ox in offs]
+    scratch = torch.empty_like(d)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    prev, it = None, 0
+    while it < 8000:
+        dpad[1:-1, 1:-1, 1:-1].copy_(d)
+        for (oz, oy, ox), wt in zip(offs, wts):
+            torch.add(dpad[1 + oz:1 + oz + nz, 1 + oy:1 + oy + ny, 1 + ox:1 + ox + nx], wt,
+                      out=scratch)
+            torch.minimum(d, scratch, out=d)
+        d.masked_fill_(solid, inf)
+        it += 1
+        if it % 64 == 0:
+            fin = torch.isfinite(d)
+            cur = (int(fin.sum()), float(d[fin].sum(dtype=torch.float64)))
+            if cur == prev:
+                break
+            prev = cur
+    torch.cuda.synchronize()
+    return it, time.perf_counter() - t0
+
+
+def bench_goal(args, dev):
+    """Goal-field bake and sampler (goalfield.py:159-298, :68-94): the GPU
+    bake of the workload's occupancy (wall time per bake; the bake reads its
+    wavefront queue length on the host every few sweeps), the reference's
+    torch sweep loop on this same GPU, the oracle's Dijkstra on one host
+    core, and the sampler at the trainer's 2048 positions and at 1 M."""
+    import numpy as np
+    import torch
+    from surfgym import goalfield, synth
+    name = args.workload if args.workload in ("ramp_field", "winding_track", "maze",
+                                               "small_ramps") else "ramp_field"
+    w = synth.goal_workload(name)
+    nz, ny, nx = w.occ.shape
+    occ_dev = torch.as_tensor(w.occ, device=dev)
+    lo, hi = goalfield.seed_voxel_box(w.zone, w.mins, w.cell, (nx, ny, nz))
+    _log(f"[bench] goal {name}: {nx}x{ny}x{nz} @{w.cell:g}u, seed box {lo.tolist()}..{hi.tolist()}")
+    field = None
+    for _ in range(max(1, args.warmup)):
+        field = goalfield.goal_field_from_occupancy(occ_dev, w.mins, w.zone, w.cell, device=dev)
+    torch.cuda.synchronize()
+    ms = []
+    for _ in range(args.steps):
+        t0 = time.perf_counter()
+        field = goalfield.goal_field_from_occupancy(occ_dev, w.mins, w.zone, w.cell, device=dev)
+        torch.cuda.synchronize()
+        ms.append((time.perf_counter() - t0) * 1e3)
+    info = field.bake_info
+    tiles = ((nx + 7) // 8) * ((ny + 7) // 8) * ((nz + 7) // 8)
+    _log(f"[bench] bake median {statistics.median(ms):.3f} ms, {info['sweeps']} sweeps, "
+         f"{info['tile_visits']} tile visits ({info['tile_visits'] / tiles:.2f} per tile)")
+    # sampler: the trainer's per-tick batch and a throughput batch
+    rng = np.random.default_rng(5)
+    hi_u = w.mins + np.array([nx, ny, nz]) * w.cell
+    samp = {}
+    for n in (2048, 1 << 20):
+        pos = torch.as_tensor(rng.uniform(w.mins, hi_u, (n, 3)), device=dev)
+        for _ in range(5):
+            field.sample(pos)
+        stream = torch.cuda.current_stream(dev)
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        reps = 200
+        torch.cuda.synchronize()
+        e0.record(stream)
+        for _ in range(reps):
+            field.sample(pos)
+        e1.record(stream)
+        torch.cuda.synchronize()
+        samp[n] = e0.elapsed_time(e1) / reps * 1e3     # us per call
+    res = {"metric": "goal-field bake ms (geodesic distance over free voxels)",
+           "value": round(statistics.median(ms), 3), "unit": "ms", "higher_is_better": False,
+           "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "dtype": "f32",
+           "data": "synthetic",
+           "config": {"workload": name, "grid": f"{nx}x{ny}x{nz}", "voxels": int(w.occ.size),
+                      "cell": w.cell, "solid_frac": round(float(w.occ.mean()), 4),
+                      "seed_voxels": info["n_seed"], "reach_max": round(info["reach_max"], 3),
+                      "sweeps": info["sweeps"], "tile_visits": info["tile_visits"],
+                      "visits_per_tile": round(info["tile_visits"] / tiles, 3)},
+           "sample": {"us_per_call_2048": round(samp[2048], 3),
+                      "us_per_call_1M": round(samp[1 << 20], 3),
+                      "G_positions_per_s_1M": round((1 << 20) / (samp[1 << 20] * 1e-6) / 1e9, 3)},
+           "reference_torch_gpu": None, "cpu_baseline": None}
+    if not args.no_ref and w.occ.size <= 64 * 1024 * 1024:
+        _log("[bench] the reference's torch sweep loop on this GPU ...")
+        sweeps, sec = _reference_goal_sweeps_torch(occ_dev, w.cell, lo, hi)
+        res["reference_torch_gpu"] = {"value": round(sec * 1e3, 1), "unit": "ms", "sweeps": sweeps,
+                                      "sample": "goalfield.py:232-270 loop as torch ops on "
+                                                "this GPU, one run"}
+    if not args.no_cpu and w.occ.size <= 64 * 1024 * 1024:
+        from oracle import goal as ogoal
+        t0 = time.perf_counter()
+        ogoal.distance(w.occ, w.cell, lo, hi)
+        cpu_s = time.perf_counter() - t0
+        res["cpu_baseline"] = {"value": round(cpu_s * 1e3, 1), "unit": "ms", "cores": 1,
+                               "kind": "port",
+                               "sample": "oracle Dijkstra (fp32, binary heap) over the whole "
+                                         "grid, one run"}
+    print(json.dumps(res), flush=True)
+
+
 def main(argv=None):
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -163,6 +287,11 @@ def main(argv=None):
     ap.add_argument("--bake", action="store_true",
                     help="time the SDF bake (GPU distance transform of the workload's "
                          "occupancy) against the reference's scipy bake instead")
+    ap.add_argument("--goal", action="store_true",
+                    help="time the goal-field bake and sampler (workloads ramp_field, "
+                         "winding_track, maze, small_ramps)")
+    ap.add_argument("--no-ref", action="store_true",
+                    help="--goal: skip the reference's torch sweep loop")
     ap.add_argument("--graph", action="store_true",
                     help="capture one render in a hipGraph and time graph replays")
     args = ap.parse_args(argv)
@@ -175,8 +304,10 @@ def main(argv=None):
     import torch
     from surfgym import synth, vision
 
-    w = synth.WORKLOADS[args.workload]
     dev = torch.device("cuda:0")
+    if args.goal:
+        return bench_goal(args, dev)
+    w = synth.WORKLOADS[args.workload]
     if args.bake:
         return bench_bake(args, w, dev)
     t0 = time.perf_counter()

@@ -34,7 +34,7 @@ extern "C" {
 
 /* Bumped on every struct or semantic change; the binding refuses a library
  * reporting another value. */
-#define SDFR_ABI_VERSION 3
+#define SDFR_ABI_VERSION 4
 
 /* Element types of caller arrays. */
 enum {
@@ -44,7 +44,8 @@ enum {
     SDFR_I32 = 3,
     SDFR_I64 = 4,
     SDFR_U8 = 5,   /* also torch.bool */
-    SDFR_F64 = 6
+    SDFR_F64 = 6,
+    SDFR_U16 = 7   /* goal-field grids */
 };
 
 /* Device layout of the handle's private copy of the grid. */
@@ -201,6 +202,55 @@ SDFR_API int32_t sdfr_edt(const uint8_t* occ, int32_t nx, int32_t ny, int32_t nz
                           void* out, int32_t out_dtype, void* workspace, int64_t workspace_size,
                           void* stream);
 SDFR_API const char* sdfr_edt_last_error(void);
+
+/* ---- Goal field ----------------------------------------------------------
+ * Geodesic distance to a goal zone over the free voxels of an occupancy grid:
+ * the reference's build_goal_field bake (python/surfgym/goalfield.py:159-298)
+ * and GoalField.sample (goalfield.py:68-94). The reference has no C ABI for
+ * either (the bake is torch tensor ops, the sampler numpy); these are the
+ * entry points its Python would bind.
+ *
+ * sdfr_goal_bake: `occ` is nz*ny*nx bytes [nz][ny][nx] on the device
+ * (nonzero = solid). Distance 0 on the free voxels of the seed box
+ * seed_lo..seed_hi (voxel indices x,y,z, inclusive, host arrays; clipped to
+ * the grid — the reference's _zone_seed_box rounding, goalfield.py:148-156,
+ * 228-231, is the caller's), relaxed over the 26 neighbours with edge cost
+ * f32(cell * |offset|) in fp32 to the exact fixpoint, solid voxels excluded.
+ * Then sentinel = reach_max + 2*cell replaces unreachable and solid voxels and
+ * the field is quantised to uint16 at quant = cell/8 (goalfield.py:272-297).
+ * Outputs (either may be NULL, not both): grid_q, the uint16 grid of the
+ * reference's cache file; grid, its f32 dequantisation u16 * quant (what
+ * GoalField holds). `workspace`: sdfr_goal_workspace_bytes() bytes of device
+ * memory, 64-byte aligned. Synchronises `stream` (the host reads the
+ * wavefront's queue length every few sweeps). Returns 0; -5 no free seed
+ * voxel, -6 sentinel beyond the uint16 range, -7 not converged within
+ * max_sweeps (sdfr_goal_last_error()). */
+typedef struct SdfrGoalInfo {
+    float reach_max;     /* largest finite geodesic distance, map units */
+    float sentinel;      /* f32(reach_max + 2*cell) */
+    float quant;         /* f32(cell / 8) */
+    int32_t sweeps;      /* wavefront sweeps that visited at least one tile */
+    int64_t n_seed;      /* free voxels in the seed box */
+    int64_t tile_visits; /* 8x8x8 tile visits over all sweeps */
+} SdfrGoalInfo;
+
+SDFR_API int64_t sdfr_goal_workspace_bytes(int32_t nx, int32_t ny, int32_t nz);
+SDFR_API int32_t sdfr_goal_bake(const uint8_t* occ, int32_t nx, int32_t ny, int32_t nz, float cell,
+                                const int32_t* seed_lo, const int32_t* seed_hi, int32_t max_sweeps,
+                                uint16_t* grid_q, float* grid, SdfrGoalInfo* info, void* workspace,
+                                int64_t workspace_size, void* stream);
+
+/* sdfr_goal_sample: trilinear distance at n positions over the honest corners
+ * (value < f32(reach_max + cell/2)) of `grid` (SDFR_F32, or SDFR_U16 read as
+ * u16 * quant), weights renormalised, f32(reach_max + 2*cell) where no corner
+ * is honest — GoalField.sample bit for bit. `pos`: device rows of 3
+ * (SDFR_F32 or SDFR_F64) at `pos_stride` elements; `mins` (host, 3 doubles)
+ * and `cell` are the grid's placement. Asynchronous on `stream`. */
+SDFR_API int32_t sdfr_goal_sample(const void* grid, int32_t grid_dtype, float quant, int32_t nx,
+                                  int32_t ny, int32_t nz, const double* mins, double cell,
+                                  double reach_max, const void* pos, int32_t pos_dtype,
+                                  int64_t pos_stride, int64_t n, float* out, void* stream);
+SDFR_API const char* sdfr_goal_last_error(void);
 
 /* Message of the calling thread's most recent error ("" if none). */
 SDFR_API const char* sdfr_last_error(void);

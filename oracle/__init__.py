@@ -4,11 +4,14 @@ Only tests/, ``__graft_entry__.smoke()`` and bench.py's CPU-baseline leg may
 import this package: it is the checker the GPU renderer is measured against,
 never part of the product path.
 
-Two restatements of the reference's render (python/surfgym/vision.py):
+Restatements of the reference's render (python/surfgym/vision.py) and of
+its goal field:
 
 * :func:`render` — per-ray C loop (``oracle/march.c``), the canonical checker.
   It also returns the number of grid loads each ray issued (the census of
   tools/bench_lidar.py:45-88), which is the algorithmic-bytes count.
+* :mod:`oracle.goal` — the goal-field bake and sampler
+  (python/surfgym/goalfield.py), ``oracle/goal.c``.
 * :mod:`oracle.lockstep` — the reference's CPU fallback shape
   (``_render_torch``, vision.py:626-666): torch tensors over all rays in
   lockstep, with a host ``any()`` check every 8 steps. It is the CPU
@@ -33,11 +36,11 @@ _lib = None
 
 
 def build(verbose: bool = False) -> Path:
-    """Compile march.c with gcc (IEEE fp32, no contraction, OpenMP)."""
+    """Compile march.c and goal.c with gcc (IEEE fp32, no contraction, OpenMP)."""
     import subprocess
     cmd = ["gcc", "-O2", "-std=c11", "-fPIC", "-shared", "-fopenmp",
            "-ffp-contract=off", "-fno-fast-math", "-fvisibility=hidden",
-           str(HERE / "march.c"), "-o", str(LIB_PATH) + ".tmp", "-lm"]
+           str(HERE / "march.c"), str(HERE / "goal.c"), "-o", str(LIB_PATH) + ".tmp", "-lm"]
     if verbose:
         print(" ".join(cmd))
     subprocess.run(cmd, check=True)
@@ -68,6 +71,13 @@ def _load():
     lib.oracle_render.restype = i
     lib.oracle_render.argtypes = [p, i, i, i, p, f, i, i, i, d, d, d, d, f, f, f, f, i,
                                   p, p, p, p, i, p, p, p, i]
+    i64 = ctypes.c_int64
+    lib.oracle_goal_distance.restype = i64
+    lib.oracle_goal_distance.argtypes = [p, i, i, i, f, p, p, p]
+    lib.oracle_goal_quantise.restype = i
+    lib.oracle_goal_quantise.argtypes = [p, i64, f, p, p, p, p, p]
+    lib.oracle_goal_sample.restype = None
+    lib.oracle_goal_sample.argtypes = [p, i, i, i, p, d, d, p, i64, p]
     _lib = lib
     return lib
 

@@ -1,8 +1,9 @@
 """Builds the native parts of the renderer in-tree.
 
-* ``lib/libsdfr.so``  — csrc/sdfr.hip (the render) and csrc/edt.hip (the
-  distance-transform bake), the HIP kernels and the C ABI of include/sdfr.h,
-  compiled for gfx950 only.
+* ``lib/libsdfr.so``  — csrc/sdfr.hip (the render), csrc/edt.hip (the
+  distance-transform bake) and csrc/goal.hip (the goal-field bake and
+  sampler), the HIP kernels and the C ABI of include/sdfr.h, compiled for
+  gfx950 only.
 * ``lib/libsurfsynth.so`` — csrc/synth.c, the host-side synthetic scene
   evaluator (gcc, OpenMP).
 
@@ -44,7 +45,7 @@ def build_sdfr(verbose: bool = False) -> Path:
     out = LIB / "libsdfr.so"
     tmp = out.with_name(out.name + ".tmp")
     _run([HIPCC, *HIP_FLAGS, "-I", str(REPO / "include"), str(PKG / "csrc" / "sdfr.hip"),
-          str(PKG / "csrc" / "edt.hip"), "-o", str(tmp)], verbose)
+          str(PKG / "csrc" / "edt.hip"), str(PKG / "csrc" / "goal.hip"), "-o", str(tmp)], verbose)
     os.replace(tmp, out)
     return out
 

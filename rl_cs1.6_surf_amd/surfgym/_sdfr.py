@@ -18,10 +18,10 @@ import torch  # noqa: F401  (load torch's HIP runtime first, see above)
 PKG_ROOT = Path(__file__).resolve().parents[1]
 LIB_PATH = PKG_ROOT / "lib" / "libsdfr.so"
 
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 # element types (SDFR_* in sdfr.h)
-F32, F16, BF16, I32, I64, U8, F64 = 0, 1, 2, 3, 4, 5, 6
+F32, F16, BF16, I32, I64, U8, F64, U16 = 0, 1, 2, 3, 4, 5, 6, 7
 LAYOUT_LINEAR, LAYOUT_BRICK4 = 0, 1
 CAM_EQUIANGULAR, CAM_PINHOLE = 0, 1
 SCHED_PERSISTENT, SCHED_TILES = 0, 1
@@ -29,7 +29,8 @@ SCHED_PERSISTENT, SCHED_TILES = 0, 1
 EXPORTS = ("sdfr_abi_version", "sdfr_last_error", "sdfr_grid_create", "sdfr_grid_destroy",
            "sdfr_grid_bytes", "sdfr_grid_attach_surfnz", "sdfr_grid_set_schedule",
            "sdfr_workspace_bytes", "sdfr_render", "sdfr_ray_dirs", "sdfr_edt_workspace_bytes",
-           "sdfr_edt", "sdfr_edt_last_error")
+           "sdfr_edt", "sdfr_edt_last_error", "sdfr_goal_workspace_bytes", "sdfr_goal_bake",
+           "sdfr_goal_sample", "sdfr_goal_last_error")
 
 
 class GridDesc(ctypes.Structure):
@@ -58,6 +59,12 @@ class Image(ctypes.Structure):
     _fields_ = [("out", ctypes.c_void_p), ("env_stride", ctypes.c_int64),
                 ("dtype", ctypes.c_int32), ("channels", ctypes.c_int32),
                 ("taps", ctypes.c_void_p)]
+
+
+class GoalInfo(ctypes.Structure):
+    _fields_ = [("reach_max", ctypes.c_float), ("sentinel", ctypes.c_float),
+                ("quant", ctypes.c_float), ("sweeps", ctypes.c_int32),
+                ("n_seed", ctypes.c_int64), ("tile_visits", ctypes.c_int64)]
 
 
 class SdfrError(RuntimeError):
@@ -106,6 +113,18 @@ def load(path: Path | str | None = None):
     lib.sdfr_edt.argtypes = [vp, i32, i32, i32, ctypes.c_float, vp, i32, vp, i64, vp]
     lib.sdfr_edt_last_error.restype = ctypes.c_char_p
     lib.sdfr_edt_last_error.argtypes = []
+    lib.sdfr_goal_workspace_bytes.restype = i64
+    lib.sdfr_goal_workspace_bytes.argtypes = [i32, i32, i32]
+    lib.sdfr_goal_bake.restype = i32
+    lib.sdfr_goal_bake.argtypes = [vp, i32, i32, i32, ctypes.c_float, ctypes.POINTER(ctypes.c_int32),
+                                   ctypes.POINTER(ctypes.c_int32), i32, vp, vp,
+                                   ctypes.POINTER(GoalInfo), vp, i64, vp]
+    lib.sdfr_goal_sample.restype = i32
+    lib.sdfr_goal_sample.argtypes = [vp, i32, ctypes.c_float, i32, i32, i32,
+                                     ctypes.POINTER(ctypes.c_double), ctypes.c_double,
+                                     ctypes.c_double, vp, i32, i64, i64, vp, vp]
+    lib.sdfr_goal_last_error.restype = ctypes.c_char_p
+    lib.sdfr_goal_last_error.argtypes = []
     got = lib.sdfr_abi_version()
     if got != ABI_VERSION:
         raise SdfrError(f"{p} reports ABI {got}, this binding mirrors ABI {ABI_VERSION}: "

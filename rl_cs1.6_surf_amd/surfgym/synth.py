@@ -343,3 +343,77 @@ WORKLOADS = {
         n_envs=8192, max_steps=96, range_units=6144.0, near_range=2000.0,
         store="f16", out_dtype="bf16"),
 }
+
+
+# --------------------------------------------------------------- goal field --
+def goal_zone(scene: Scene) -> dict:
+    """A goal box ({"mins", "maxs"}, map units, the reference's zone format):
+    96 x 96 x 64 u centred 80 u above the last ramp of a track scene, or over
+    the ground near the far corner of a ramp scene."""
+    if scene.boxes.size == 0 and len(scene.prisms) > 100:        # a track: its last segment
+        p = scene.prisms[-1]
+        c = np.array([p["cx"], p["cy"], p["z0"] + p["height"] + 80.0], np.float64)
+    else:
+        ext = scene.extent
+        c = scene.mins.astype(np.float64) + np.array([0.92 * ext[0], 0.92 * ext[1], 0.0])
+        c[2] = float(scene.ground_z) + 96.0
+    h = np.array([48.0, 48.0, 32.0])
+    return {"mins": (c - h).tolist(), "maxs": (c + h).tolist()}
+
+
+def maze_occupancy(nx: int, ny: int, nz: int, seed: int, *, room: int = 8, storey: int = 16):
+    """A 3-D labyrinth [nz, ny, nx] uint8 (1 = solid): walls every ``room``
+    voxels along x and y with one 2x3-voxel doorway per wall segment, and a
+    floor every ``storey`` voxels along z with one 2x2 hole per room — long
+    winding geodesics for the goal-field bake."""
+    rng = np.random.default_rng(seed)
+    occ = np.zeros((nz, ny, nx), np.uint8)
+    occ[:, :, ::room] = 1
+    occ[:, ::room, :] = 1
+    for z0 in range(0, nz, storey):
+        occ[z0, :, :] = 1
+    rx, ry = (nx + room - 1) // room, (ny + room - 1) // room
+    for z0 in range(0, nz, storey):
+        z1 = min(z0 + storey, nz)
+        for j in range(ry):
+            for i in range(rx):
+                x0, y0 = i * room, j * room
+                # doorway in the x-wall (plane x = x0) and in the y-wall (plane y = y0)
+                if z1 - z0 > 4:
+                    dz = int(rng.integers(z0 + 1, z1 - 3))
+                    dy = int(rng.integers(y0 + 1, min(y0 + room - 2, ny - 2) + 1))
+                    occ[dz:dz + 3, dy:dy + 2, x0] = 0
+                    dx = int(rng.integers(x0 + 1, min(x0 + room - 2, nx - 2) + 1))
+                    occ[dz:dz + 3, y0, dx:dx + 2] = 0
+                if z0 > 0 and rng.random() < 0.5:
+                    hx = int(rng.integers(x0 + 1, min(x0 + room - 2, nx - 2) + 1))
+                    hy = int(rng.integers(y0 + 1, min(y0 + room - 2, ny - 2) + 1))
+                    occ[z0, hy:hy + 2, hx:hx + 2] = 0
+    return occ
+
+
+@dataclass
+class GoalWorkload:
+    """An occupancy grid, its placement and a goal zone."""
+    name: str
+    occ: np.ndarray
+    mins: np.ndarray
+    cell: float
+    zone: dict
+
+
+def goal_workload(name: str) -> GoalWorkload:
+    """ramp_field / winding_track: the render scenes' solid voxels with
+    goal_zone(); maze: maze_occupancy(256, 256, 64) at 16 u, goal in the
+    far top corner room."""
+    if name in ("ramp_field", "winding_track", "small_ramps"):
+        sc = WORKLOADS[name].scene()
+        occ = (sc.sdf == 0).astype(np.uint8)
+        return GoalWorkload(name, occ, sc.mins.astype(np.float64), sc.cell, goal_zone(sc))
+    if name == "maze":
+        occ = maze_occupancy(256, 256, 64, 3000)
+        mins = np.zeros(3)
+        c = np.array([252.0, 252.0, 60.0]) * 16.0
+        return GoalWorkload(name, occ, mins, 16.0,
+                            {"mins": (c - 24.0).tolist(), "maxs": (c + 24.0).tolist()})
+    raise KeyError(f"unknown goal workload {name!r}")

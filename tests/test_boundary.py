@@ -41,7 +41,8 @@ def test_binding_structs_match_the_header_layout(tmp_path):
     import subprocess
     from surfgym import _sdfr
     structs = {"SdfrGridDesc": _sdfr.GridDesc, "SdfrCam": _sdfr.Cam,
-               "SdfrPoses": _sdfr.Poses, "SdfrImage": _sdfr.Image}
+               "SdfrPoses": _sdfr.Poses, "SdfrImage": _sdfr.Image,
+               "SdfrGoalInfo": _sdfr.GoalInfo}
     lines = ['#include <stdio.h>', '#include <stddef.h>', '#include "sdfr.h"', "int main(void){"]
     for cname, cls in structs.items():
         lines.append(f'printf("{cname} size %zu\\n", sizeof({cname}));')
@@ -84,7 +85,7 @@ def test_grid_create_rejects_bad_descriptors_without_a_device():
     for desc, dtype, store, layout, needle in [
         (_sdfr.GridDesc(0, 2, 2, (ctypes.c_float * 3)(), 16.0), 0, 0, 0, "positive"),
         (_sdfr.GridDesc(2, 2, 2, (ctypes.c_float * 3)(), 0.0), 0, 0, 0, "cell"),
-        (_sdfr.GridDesc(2, 2, 2, (ctypes.c_float * 3)(), 16.0), 7, 0, 0, "source dtype"),
+        (_sdfr.GridDesc(2, 2, 2, (ctypes.c_float * 3)(), 16.0), 42, 0, 0, "source dtype"),
         (_sdfr.GridDesc(2, 2, 2, (ctypes.c_float * 3)(), 16.0), 0, 2, 0, "store dtype"),
         (_sdfr.GridDesc(2, 2, 2, (ctypes.c_float * 3)(), 16.0), 0, 0, 9, "layout"),
     ]:
@@ -155,3 +156,96 @@ def test_grid_contract_helpers():
     assert (nx, ny, nz) == (133, 133, 69)
     assert vision.pick_cell(Core()) == 16.0
     assert vision.pick_cell(Core(), budget_voxels=1e5) == 64.0
+
+
+def test_goal_entry_points_reject_bad_arguments_without_a_device():
+    from surfgym import _sdfr
+    lib = _sdfr.load()
+    assert lib.sdfr_goal_workspace_bytes(0, 4, 4) < 0
+    ws = lib.sdfr_goal_workspace_bytes(17, 9, 8)
+    tiles = 3 * 2 * 1
+    assert ws >= 17 * 9 * 8 * 4 + 4 * tiles * 4
+    info = _sdfr.GoalInfo()
+    lo = (ctypes.c_int32 * 3)(0, 0, 0)
+    hi = (ctypes.c_int32 * 3)(1, 1, 1)
+    fake = 64 * 1024   # never dereferenced: every case fails before a launch
+    cases = [
+        (dict(occ=None), -1, "null"),
+        (dict(grid_q=None, grid=None), -1, "null"),
+        (dict(nx=0), -2, "positive"),
+        (dict(cell=0.0), -2, "cell"),
+        (dict(max_sweeps=0), -2, "max_sweeps"),
+        (dict(size=16), -2, "workspace"),
+        (dict(ws=fake + 4), -2, "aligned"),
+        (dict(hi=(ctypes.c_int32 * 3)(-1, 1, 1)), -5, "no free voxel"),
+    ]
+    for kw, code, needle in cases:
+        a = dict(occ=fake, nx=17, ny=9, nz=8, cell=16.0, lo=lo, hi=hi, max_sweeps=100,
+                 grid_q=fake, grid=None, ws=fake, size=ws)
+        a.update(kw)
+        rc = lib.sdfr_goal_bake(a["occ"], a["nx"], a["ny"], a["nz"], a["cell"], a["lo"], a["hi"],
+                                a["max_sweeps"], a["grid_q"], a["grid"], ctypes.byref(info),
+                                a["ws"], a["size"], None)
+        msg = lib.sdfr_goal_last_error().decode()
+        assert rc == code and needle in msg, (kw, rc, msg)
+    mins = (ctypes.c_double * 3)(0.0, 0.0, 0.0)
+    for args, code, needle in [
+        ((fake, 42, 1.0, 4, 4, 4, mins, 16.0, 100.0, fake, _sdfr.F64, 3, 1, fake), -3, "grid dtype"),
+        ((fake, _sdfr.F32, 1.0, 4, 4, 4, mins, 16.0, 100.0, fake, _sdfr.I32, 3, 1, fake), -3,
+         "position dtype"),
+        ((fake, _sdfr.F32, 1.0, 4, 4, 4, mins, 16.0, 100.0, fake, _sdfr.F64, 2, 1, fake), -2,
+         "stride"),
+        ((fake, _sdfr.F32, 1.0, 0, 4, 4, mins, 16.0, 100.0, fake, _sdfr.F64, 3, 1, fake), -2,
+         "dims"),
+        ((None, _sdfr.F32, 1.0, 4, 4, 4, mins, 16.0, 100.0, fake, _sdfr.F64, 3, 1, fake), -1,
+         "null"),
+    ]:
+        rc = lib.sdfr_goal_sample(*args, None)
+        msg = lib.sdfr_goal_last_error().decode()
+        assert rc == code and needle in msg, (rc, msg)
+    assert lib.sdfr_goal_sample(fake, _sdfr.F32, 1.0, 4, 4, 4, mins, 16.0, 100.0, None, _sdfr.F64,
+                                3, 0, fake, None) == 0
+
+
+def test_goal_seed_box_and_cache_contract(tmp_path):
+    """The seed box rounding (goalfield.py:148-156, :228-231) by hand, the
+    cache signature format (:173-177), and the refusals of the host layer."""
+    from surfgym import goalfield
+    # a zone shrunk to the centre of voxel 5 (88 u at cell 16): grown by 20 u
+    # to [68, 108] -> floor(68/16 - .5) = 3, ceil(108/16 - .5) = 7
+    z = {"mins": [88.0, 88.0, 88.0], "maxs": [88.0, 88.0, 88.0]}
+    lo, hi = goalfield.seed_voxel_box(z, np.zeros(3), 16.0, (20, 20, 20))
+    assert lo.tolist() == [3, 3, 3] and hi.tolist() == [7, 7, 7]
+    # cell 64 grows by 48 u: [40, 136] -> floor(.125) = 0, ceil(1.625) = 2; clipped to the grid
+    lo, hi = goalfield.seed_voxel_box(z, np.zeros(3), 64.0, (2, 9, 9))
+    assert lo.tolist() == [0, 0, 0] and hi.tolist() == [1, 2, 2]
+    # below the grid: lo clips to 0, hi stays negative (an empty box)
+    lo, hi = goalfield.seed_voxel_box({"mins": [-900.0] * 3, "maxs": [-800.0] * 3},
+                                      np.zeros(3), 16.0, (8, 8, 8))
+    assert lo.tolist() == [0, 0, 0] and np.all(hi < 0)
+
+    bsp = tmp_path / "surf_x.bsp"
+    bsp.write_bytes(b"BSP" * 10)
+    st = bsp.stat()
+    zone = {"mins": [1.04, -2.0, 3.0], "maxs": [10.0, 20.0, 30.55]}
+    sig = goalfield._goal_sig(bsp, zone, False)
+    assert sig == f"g4_v2_{st.st_size}_{st.st_mtime_ns}_1_-2_3_10_20_30.6"
+    assert goalfield._goal_sig(bsp, zone, True).startswith("g4_k1_v2_")
+
+    class Core:
+        bsp_path = str(bsp)
+
+    with pytest.raises(FileNotFoundError, match="slabocc"):
+        goalfield.build_goal_field(Core(), zone, 16.0)
+    with pytest.raises(NotImplementedError):
+        goalfield.build_goal_field(Core(), zone, 16.0, mask_kill=True)
+    np.savez(tmp_path / "surf_x.slabocc_16.npz", occ=np.zeros((2, 2, 2), np.uint8),
+             mins=np.zeros(3), sig=np.str_("stale"))
+    with pytest.raises(FileNotFoundError, match="stale"):
+        goalfield.build_goal_field(Core(), zone, 16.0)
+    with pytest.raises(ValueError, match="no CPU path"):
+        goalfield.GoalField(np.zeros((2, 2, 2), np.float32), np.zeros(3), 16.0, 10.0,
+                            device="cpu")
+    with pytest.raises(ValueError, match="no CPU path"):
+        goalfield.goal_field_from_occupancy(np.zeros((2, 2, 2)), np.zeros(3), zone, 16.0,
+                                            device="cpu")
