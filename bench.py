@@ -277,9 +277,11 @@ def main(argv=None):
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--workload", default="ramp_field")
     ap.add_argument("--layout", default="brick4", choices=["brick4", "linear"])
-    ap.add_argument("--schedule", default="tiles", choices=["persistent", "tiles"])
+    ap.add_argument("--schedule", default="tiles", choices=["persistent", "tiles", "slots"])
     ap.add_argument("--refill", type=int, default=16, help="free lanes that trigger a refill")
-    ap.add_argument("--rpl", type=int, default=2, help="tiles schedule: rays per lane (1, 2, 4)")
+    ap.add_argument("--rpl", type=int, default=None,
+                    help="rays per lane: tiles 1-2, slots 1-4 (default: the library's choice, "
+                         "2 for cache-resident grids, 1 above 192 MiB)")
     ap.add_argument("--cpu-envs", type=int, default=2048,
                     help="envs of the workload the CPU baseline renders (default: all of ramp_field)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
@@ -387,7 +389,7 @@ def main(argv=None):
          f"launch avg {avg_launch_ms:.4f} ms, median {med_launch_ms:.4f} ms")
 
     copy_gbs = None if args.no_copy else copy_bandwidth(dev)
-    traffic = profiled_traffic(f"{w.name} {args.schedule} rpl={args.rpl} {args.layout} {w.store}")
+    traffic = profiled_traffic(f"{w.name} {args.schedule} rpl={lid.rays_per_lane} {args.layout} {w.store}")
     if copy_gbs:
         _log(f"[bench] device copy {copy_gbs:.0f} GB/s")
     res = {
@@ -406,7 +408,7 @@ def main(argv=None):
         "config": {"workload": w.name, "envs": n, "image": f"{w.width}x{w.height}",
                    "rays": rays, "grid": f"{sc.nx}x{sc.ny}x{sc.nz} {w.store} @{sc.cell:g}u",
                    "layout": args.layout, "schedule": args.schedule, "refill_lanes": args.refill,
-                   "rays_per_lane": args.rpl,
+                   "rays_per_lane": lid.rays_per_lane,
                    "out": w.out_dtype, "max_steps": w.max_steps,
                    "hit_eps": w.hit_eps, "range": round(w.range_units, 3),
                    "near": round(w.near_range, 3), "grid_loads_per_ray": round(loads / rays, 4),

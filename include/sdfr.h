@@ -34,7 +34,7 @@ extern "C" {
 
 /* Bumped on every struct or semantic change; the binding refuses a library
  * reporting another value. */
-#define SDFR_ABI_VERSION 4
+#define SDFR_ABI_VERSION 5
 
 /* Element types of caller arrays. */
 enum {
@@ -63,7 +63,8 @@ enum {
 /* Work schedules of sdfr_render (both give identical results). */
 enum {
     SDFR_SCHED_PERSISTENT = 0, /* persistent waves refilling ended rays' lanes */
-    SDFR_SCHED_TILES = 1       /* default: launch-scheduled waves of 8x8 pixel tiles */
+    SDFR_SCHED_TILES = 1,      /* default: launch-scheduled waves of 8x8 pixel tiles */
+    SDFR_SCHED_SLOTS = 2       /* persistent waves of R tile slots, a drained slot takes a new tile */
 };
 
 /* Grid geometry: the reference's single grid definition, grid_dims()
@@ -150,9 +151,9 @@ SDFR_API int32_t sdfr_grid_attach_surfnz(SdfrGrid* grid, const void* src, int32_
 /* Chooses how sdfr_render schedules rays on this handle: `schedule` is an
  * SDFR_SCHED_* value (default SDFR_SCHED_TILES); `refill_lanes` (1..64,
  * default 16) is the number of free lanes at which a persistent wave takes
- * new rays; `rays_per_lane` (1 or 2, default 2) is how many tiles a wave
- * of the tiles schedule marches at once. Surf-mask renders always use the
- * tiles schedule. Results do not depend on any of them. No reference
+ * new rays; `rays_per_lane` is how many tiles a wave marches at once: 1 or
+ * 2 (default 2) for the tiles schedule, 1..4 slots for the slots schedule.
+ * Surf-mask renders always use the tiles schedule. Results do not depend on any of them. No reference
  * counterpart: the Triton launch has one fixed shape (vision.py:48-54;
  * tools/proto_march.py sweeps it). */
 SDFR_API int32_t sdfr_grid_set_schedule(SdfrGrid* grid, int32_t schedule, int32_t refill_lanes,

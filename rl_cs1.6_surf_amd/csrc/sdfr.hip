@@ -64,6 +64,8 @@ constexpr int kMaxAxisEntries = 16384;
 constexpr int kParts = 8;
 constexpr int kCtrStride = 32;
 constexpr int kCounterWords = (kParts + 1) * kCtrStride;
+// Grids up to this size stay resident in the 256 MB Infinity Cache.
+constexpr int64_t kCacheResidentBytes = 192ll << 20;
 
 // ---------------------------------------------------------------- errors --
 thread_local char g_err[512];
@@ -195,6 +197,8 @@ __device__ __forceinline__ float2 sincos_f32(float x) {
 struct MarchArgs {
     const void* grid;
     uint32_t grid_bytes;          // size of the device copy (the descriptor's range)
+    uint32_t dead_off;            // gather offset for ended rays: past the range, reads 0
+                                  // without touching memory
     int nx, ny, nz, bx, by, layout;
     float fnx1, fny1, fnz1;       // n-1 as float: the clamp bound
     float mnx, mny, mnz, inv_cell;
@@ -336,8 +340,8 @@ __global__ __launch_bounds__(256) void ray_tables_kernel(MarchArgs a) {
 // of them. Per step a lane issues the gathers of all its live rays before
 // using any, so RPL independent loads per lane are in flight at once — the
 // march is bound by gather latency, and this multiplies the loads in flight
-// without more waves. Lanes of dead rays point their load at offset 0 (all at
-// one address), which costs one cache line per wave-step.
+// without more waves. Lanes of dead rays point their load past the end of
+// the buffer range, where the hardware returns 0 without a cache access.
 //
 // The step counter is wave-uniform and the loop leaves as soon as no ray of
 // the wave is alive, which is exact: alive only turns off and a dead ray adds
@@ -411,7 +415,7 @@ __global__ __launch_bounds__(256) void march_tiles(MarchArgs a) {
             const int ix = (int)__builtin_amdgcn_fmed3f((px - a.mnx) * a.inv_cell, 0.0f, a.fnx1);
             const int iy = (int)__builtin_amdgcn_fmed3f((py - a.mny) * a.inv_cell, 0.0f, a.fny1);
             const int iz = (int)__builtin_amdgcn_fmed3f((pz - a.mnz) * a.inv_cell, 0.0f, a.fnz1);
-            const uint32_t off = alive[j] ? tab[ix] + tab[a.nx + iy] + tab[a.nx + a.ny + iz] : 0u;
+            const uint32_t off = alive[j] ? tab[ix] + tab[a.nx + iy] + tab[a.nx + a.ny + iz] : a.dead_off;
             sd[j] = load_voxel<GT>(rsrc, off);
         }
 #pragma unroll
@@ -585,6 +589,139 @@ __global__ __launch_bounds__(256) void march_persistent(MarchArgs a) {
     }
 }
 
+// ------------------------------------------------------ schedule: slots --
+// A grid that fills every CU once; each wave marches R independent 8x8 pixel
+// tiles ("slots"), one ray per lane per slot. A slot whose 64 rays have all
+// ended writes them and takes the wave's next tile, so a wave keeps R
+// coherent gathers in flight until its tiles are done: the tiles schedule's
+// coherence without its coupling of R tiles to the slowest ray among them.
+// Tiles are dealt statically: the waves of XCD x (blocks x, x+8, ...) stride
+// through the x-th eighth of the tile range in step, so an XCD works on a
+// few consecutive envs at a time; no atomics, no counters.
+struct TileSource {
+    int next;    // the wave's next tile
+    int stride;  // waves sharing the partition
+    int end;     // end of the partition
+};
+
+__device__ __forceinline__ int take_tile(TileSource& src) {
+    if (src.next >= src.end) return -1;
+    const int tile = src.next;
+    src.next += src.stride;
+    return tile;
+}
+
+__device__ __forceinline__ float uniform_f(float v) {
+    return __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(v)));
+}
+
+template <typename GT, int LAYOUT, int OUT_DTYPE, int CAMERA, bool CENSUS, int R>
+__global__ __launch_bounds__(256) void march_slots(MarchArgs a) {
+    extern __shared__ uint32_t s_axis[];
+    fill_axis_tables<GT, LAYOUT>(a, s_axis);
+    const int lane = threadIdx.x & 63;
+    const int lr = lane >> 3, lc = lane & 7;
+    const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<void*>(a.grid), 0, (int)a.grid_bytes, kRsrcWord3);
+    const uint32_t* __restrict__ tab = s_axis;
+    // this wave's place among the waves of its XCD's partition
+    const int total = (int)a.total_tiles;
+    TileSource src;
+    {
+        const int q = a.nblocks >> 3, rem = a.nblocks & 7;
+        const int x = (int)(blockIdx.x & 7);
+        const int nb = q + (x < rem ? 1 : 0);            // blocks on this partition
+        const int lw = (int)(blockIdx.x >> 3) * 4 + (int)(threadIdx.x >> 6);
+        const int lo = (int)((int64_t)total * x / kParts);
+        src.end = (int)((int64_t)total * (x + 1) / kParts);
+        src.next = __builtin_amdgcn_readfirstlane(lo + lw);
+        src.stride = nb * 4;
+    }
+
+    // per slot: wave-uniform eye, tile and step count (scalar registers),
+    // per-lane direction, depth and liveness
+    float ex[R], ey[R], ez[R], dx[R], dy[R], dz[R], t[R];
+    bool alive[R];
+    int tl[R], steps[R], taps[R];
+    auto start = [&](int j) {
+        tl[j] = take_tile(src);
+        if (tl[j] < 0) return;
+        const int n = tl[j] / a.tiles_per_env;
+        const int rem = tl[j] - n * a.tiles_per_env;
+        const int ty = rem / a.tiles_x;
+        const int r = ty * 8 + lr, c = (rem - ty * a.tiles_x) * 8 + lc;
+        const float2* rt = a.rt + (int64_t)n * a.rt_stride;
+        const float2 e01 = rt[a.H + a.W], e2 = rt[a.H + a.W + 1];
+        float2 psc = make_float2(0.f, 0.f), ysc = make_float2(0.f, 0.f);
+        if constexpr (CAMERA == SDFR_CAM_PINHOLE) {
+            psc = rt[a.H + a.W + 2];
+            ysc = rt[a.H + a.W + 3];
+        }
+        const float3 d = ray_dir<CAMERA>(rt[min(r, a.H - 1)], rt[a.H + min(c, a.W - 1)], psc, ysc);
+        ex[j] = uniform_f(e01.x);
+        ey[j] = uniform_f(e01.y);
+        ez[j] = uniform_f(e2.x);
+        dx[j] = d.x;
+        dy[j] = d.y;
+        dz[j] = d.z;
+        t[j] = 0.0f;
+        taps[j] = 0;
+        steps[j] = 0;
+        alive[j] = r < a.H && c < a.W && a.max_steps > 0;
+    };
+    // slot j's rays have all ended: write them
+    auto finish = [&](int j) {
+        const int n = tl[j] / a.tiles_per_env;
+        const int rem = tl[j] - n * a.tiles_per_env;
+        const int ty = rem / a.tiles_x;
+        const int r = ty * 8 + lr, c = (rem - ty * a.tiles_x) * 8 + lc;
+        if (r < a.H && c < a.W) {
+            const int pix = r * a.W + c;
+            const int64_t o = (int64_t)n * a.env_stride + pix;
+            store_enc<OUT_DTYPE>(a.out, o, encode_depth(fminf(t[j], a.rng), a.near));
+            if constexpr (CENSUS) a.taps[(int64_t)n * a.H * a.W + pix] = taps[j];
+        }
+    };
+#pragma unroll
+    for (int j = 0; j < R; ++j) start(j);
+    while (true) {
+        bool any_act = false;
+#pragma unroll
+        for (int j = 0; j < R; ++j) any_act |= tl[j] >= 0;
+        if (!any_act) break;
+        float sd[R];
+#pragma unroll
+        for (int j = 0; j < R; ++j) {
+            sd[j] = 0.0f;
+            if (tl[j] >= 0) {
+                const float px = ex[j] + dx[j] * t[j];
+                const float py = ey[j] + dy[j] * t[j];
+                const float pz = ez[j] + dz[j] * t[j];
+                const int ix = (int)__builtin_amdgcn_fmed3f((px - a.mnx) * a.inv_cell, 0.0f, a.fnx1);
+                const int iy = (int)__builtin_amdgcn_fmed3f((py - a.mny) * a.inv_cell, 0.0f, a.fny1);
+                const int iz = (int)__builtin_amdgcn_fmed3f((pz - a.mnz) * a.inv_cell, 0.0f, a.fnz1);
+                const uint32_t off = alive[j] ? tab[ix] + tab[a.nx + iy] + tab[a.nx + a.ny + iz] : a.dead_off;
+                sd[j] = load_voxel<GT>(rsrc, off);
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < R; ++j) {
+            if (tl[j] < 0) continue;
+            if (alive[j]) {
+                if constexpr (CENSUS) ++taps[j];
+                alive[j] = (sd[j] > a.hit_eps) && (t[j] < a.rng);
+                if (alive[j]) t[j] = t[j] + fmaxf(sd[j] * 0.9f, a.min_step);
+            }
+            ++steps[j];
+            if (steps[j] >= a.max_steps) alive[j] = false;
+            if (!__any(alive[j])) {
+                finish(j);
+                start(j);
+            }
+        }
+    }
+}
+
 // ----------------------------------------------------------- directions --
 // One thread per ray: the directions the march casts, (N,H,W,3) f32, from the
 // same table entries and the same ray_dir().
@@ -671,6 +808,43 @@ void launch_tiles(MarchArgs& a, int rpl, hipStream_t st) {
     else march_tiles<GT, LAYOUT, OUT, CAMERA, CENSUS, 1, SURF><<<a.nblocks, 256, lds, st>>>(a);
 }
 
+// A grid that fills every CU once (never more waves than tiles) for a
+// schedule whose waves drain the per-XCD tile stream.
+template <typename K>
+int persistent_blocks(K kernel, const MarchArgs& a, const SdfrGrid* g, size_t lds, int tiles_per_wave) {
+    int per_cu = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, reinterpret_cast<const void*>(kernel), 256,
+                                                     lds) != hipSuccess ||
+        per_cu <= 0)
+        per_cu = 1;
+    const int64_t want = (int64_t)per_cu * (g->cus > 0 ? g->cus : 1);
+    const int64_t need = (a.total_tiles + 4 * tiles_per_wave - 1) / (4 * tiles_per_wave);
+    // at least one block per XCD partition: every partition's tiles need waves
+    return (int)(want < need ? (want > 8 ? want : 8) : (need > 8 ? need : 8));
+}
+
+template <typename GT, int LAYOUT, int OUT, int CAMERA, bool CENSUS>
+void launch_slots(MarchArgs& a, const SdfrGrid* g, size_t lds, hipStream_t st) {
+    switch (g->rays_per_lane) {
+    case 1:
+        a.nblocks = persistent_blocks(march_slots<GT, LAYOUT, OUT, CAMERA, CENSUS, 1>, a, g, lds, 1);
+        march_slots<GT, LAYOUT, OUT, CAMERA, CENSUS, 1><<<a.nblocks, 256, lds, st>>>(a);
+        break;
+    case 2:
+        a.nblocks = persistent_blocks(march_slots<GT, LAYOUT, OUT, CAMERA, CENSUS, 2>, a, g, lds, 2);
+        march_slots<GT, LAYOUT, OUT, CAMERA, CENSUS, 2><<<a.nblocks, 256, lds, st>>>(a);
+        break;
+    case 3:
+        a.nblocks = persistent_blocks(march_slots<GT, LAYOUT, OUT, CAMERA, CENSUS, 3>, a, g, lds, 3);
+        march_slots<GT, LAYOUT, OUT, CAMERA, CENSUS, 3><<<a.nblocks, 256, lds, st>>>(a);
+        break;
+    default:
+        a.nblocks = persistent_blocks(march_slots<GT, LAYOUT, OUT, CAMERA, CENSUS, 4>, a, g, lds, 4);
+        march_slots<GT, LAYOUT, OUT, CAMERA, CENSUS, 4><<<a.nblocks, 256, lds, st>>>(a);
+        break;
+    }
+}
+
 template <typename GT, int LAYOUT, int OUT, int CAMERA, bool CENSUS>
 void launch_march(MarchArgs& a, const SdfrGrid* g, bool surf, hipStream_t st) {
     if (surf) {
@@ -685,6 +859,10 @@ void launch_march(MarchArgs& a, const SdfrGrid* g, bool surf, hipStream_t st) {
         return;
     }
     const size_t lds = axis_lds_bytes(a);
+    if (g->schedule == SDFR_SCHED_SLOTS) {
+        launch_slots<GT, LAYOUT, OUT, CAMERA, CENSUS>(a, g, lds, st);
+        return;
+    }
     // a grid that fills every CU once, never more blocks than the tiles need
     int per_cu = 0;
     if (hipOccupancyMaxActiveBlocksPerMultiprocessor(
@@ -870,7 +1048,9 @@ SDFR_API SdfrGrid* sdfr_grid_create(const SdfrGridDesc* desc, const void* src, i
     g->nz_bytes = 0;
     g->schedule = SDFR_SCHED_TILES;
     g->refill_lanes = 16;
-    g->rays_per_lane = 2;
+    // two tiles per wave while the grid is cache-resident; one when it spills
+    // to HBM, where fewer rays in flight thrash fewer DRAM pages
+    g->rays_per_lane = g->bytes > kCacheResidentBytes ? 1 : 2;
     g->cus = 0;
     hipError_t e = hipGetDevice(&g->device);
     if (e == hipSuccess)
@@ -954,14 +1134,16 @@ SDFR_API int32_t sdfr_grid_set_schedule(SdfrGrid* grid, int32_t schedule, int32_
                                         int32_t rays_per_lane) {
     g_err[0] = '\0';
     if (!grid) return fail(-1, "sdfr_grid_set_schedule: null grid handle");
-    if (schedule != SDFR_SCHED_PERSISTENT && schedule != SDFR_SCHED_TILES)
+    if (schedule != SDFR_SCHED_PERSISTENT && schedule != SDFR_SCHED_TILES &&
+        schedule != SDFR_SCHED_SLOTS)
         return fail(-3, "sdfr_grid_set_schedule: unknown schedule %d", schedule);
     if (refill_lanes < 1 || refill_lanes > 64)
         return fail(-2, "sdfr_grid_set_schedule: refill_lanes must be in 1..64 (got %d)",
                     refill_lanes);
-    if (rays_per_lane != 1 && rays_per_lane != 2)
-        return fail(-2, "sdfr_grid_set_schedule: rays_per_lane must be 1 or 2 (got %d)",
-                    rays_per_lane);
+    const int max_rpl = schedule == SDFR_SCHED_SLOTS ? 4 : 2;
+    if (rays_per_lane < 1 || rays_per_lane > max_rpl)
+        return fail(-2, "sdfr_grid_set_schedule: rays_per_lane must be in 1..%d for this schedule "
+                    "(got %d)", max_rpl, rays_per_lane);
     grid->schedule = schedule;
     grid->refill_lanes = refill_lanes;
     grid->rays_per_lane = rays_per_lane;
@@ -1001,6 +1183,9 @@ SDFR_API int32_t sdfr_render(const SdfrGrid* grid, const SdfrCam* cam, const Sdf
     a.rt = (float2*)workspace;
     a.grid = grid->data;
     a.grid_bytes = (uint32_t)grid->bytes;
+    // an offset at the end of the range is out of range for a 4-byte read;
+    // near 4 GiB fall back to offset 0, an ordinary in-range read
+    a.dead_off = grid->bytes <= 0xffffff00ll ? (uint32_t)grid->bytes : 0u;
     a.nx = grid->desc.nx;
     a.ny = grid->desc.ny;
     a.nz = grid->desc.nz;

@@ -18,13 +18,13 @@ import torch  # noqa: F401  (load torch's HIP runtime first, see above)
 PKG_ROOT = Path(__file__).resolve().parents[1]
 LIB_PATH = PKG_ROOT / "lib" / "libsdfr.so"
 
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 # element types (SDFR_* in sdfr.h)
 F32, F16, BF16, I32, I64, U8, F64, U16 = 0, 1, 2, 3, 4, 5, 6, 7
 LAYOUT_LINEAR, LAYOUT_BRICK4 = 0, 1
 CAM_EQUIANGULAR, CAM_PINHOLE = 0, 1
-SCHED_PERSISTENT, SCHED_TILES = 0, 1
+SCHED_PERSISTENT, SCHED_TILES, SCHED_SLOTS = 0, 1, 2
 
 EXPORTS = ("sdfr_abi_version", "sdfr_last_error", "sdfr_grid_create", "sdfr_grid_destroy",
            "sdfr_grid_bytes", "sdfr_grid_attach_surfnz", "sdfr_grid_set_schedule",

@@ -46,7 +46,8 @@ _DUCK_DTYPES = {torch.float32: _sdfr.F32, torch.float16: _sdfr.F16, torch.bfloat
 _GRID_DTYPES = {torch.float32: _sdfr.F32, torch.float16: _sdfr.F16}
 _OUT_DTYPES = {torch.float32: _sdfr.F32, torch.bfloat16: _sdfr.BF16}
 _LAYOUTS = {"linear": _sdfr.LAYOUT_LINEAR, "brick4": _sdfr.LAYOUT_BRICK4}
-_SCHEDULES = {"persistent": _sdfr.SCHED_PERSISTENT, "tiles": _sdfr.SCHED_TILES}
+_SCHEDULES = {"persistent": _sdfr.SCHED_PERSISTENT, "tiles": _sdfr.SCHED_TILES,
+              "slots": _sdfr.SCHED_SLOTS}
 
 
 def pick_cell(core, budget_voxels: float = 700e6) -> float:
@@ -156,9 +157,11 @@ class GpuLidar:
       0.3*cell by default (vision.py:87-88);
     * ``schedule`` / ``refill_lanes`` / ``rays_per_lane`` — how the kernel
       schedules rays: launch-scheduled waves of 8x8 pixel "tiles", each lane
-      marching ``rays_per_lane`` rays at once (default, 2), or "persistent"
-      waves that refill lanes with new rays once ``refill_lanes`` of them
-      have finished. The results are identical.
+      marching ``rays_per_lane`` rays at once (default: 2 for grids that fit
+      the Infinity Cache, 1 above 192 MiB); "slots", persistent waves holding
+      ``rays_per_lane`` (1-4) tiles that each take a new tile when their 64
+      rays end; or "persistent" waves that refill lanes with new rays once
+      ``refill_lanes`` of them have finished. The results are identical.
     """
 
     def __init__(self, core, width: int = 128, height: int = 64,
@@ -169,7 +172,7 @@ class GpuLidar:
                  pinhole: bool = False, *, grid_dtype=torch.float16,
                  layout: str = "brick4", hit_eps: float = None,
                  min_step: float = None, schedule: str = "tiles",
-                 refill_lanes: int = 16, rays_per_lane: int = 2, _grid=None,
+                 refill_lanes: int = 16, rays_per_lane: int | None = None, _grid=None,
                  _surf_nz=None) -> None:
         if surf_mask and pinhole:
             raise ValueError(
@@ -267,8 +270,12 @@ class GpuLidar:
         self.set_schedule(schedule, refill_lanes, rays_per_lane)
 
     def set_schedule(self, schedule: str = "tiles", refill_lanes: int = 16,
-                     rays_per_lane: int = 2) -> None:
-        """Switch the ray schedule of later renders (results are unchanged)."""
+                     rays_per_lane: int | None = None) -> None:
+        """Switch the ray schedule of later renders (results are unchanged).
+        ``rays_per_lane=None`` picks 2 while the grid fits the Infinity Cache
+        and 1 above 192 MiB, as the library does for a new grid."""
+        if rays_per_lane is None:
+            rays_per_lane = 1 if self.grid_bytes > (192 << 20) else 2
         if schedule not in _SCHEDULES:
             raise ValueError(f"schedule must be one of {sorted(_SCHEDULES)}, got {schedule!r}")
         _sdfr.check(self._lib.sdfr_grid_set_schedule(self._grid, _SCHEDULES[schedule],
