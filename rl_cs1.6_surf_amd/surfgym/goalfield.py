@@ -25,7 +25,7 @@ from pathlib import Path
 import numpy as np
 import torch
 
-from . import _sdfr
+from . import _sdfr, vision
 
 __all__ = ["GoalField", "build_goal_field", "goal_field_from_occupancy", "zone_seed_box",
            "seed_voxel_box"]
@@ -33,15 +33,8 @@ __all__ = ["GoalField", "build_goal_field", "goal_field_from_occupancy", "zone_s
 # the reference's cache versioning (goalfield.py:44-47): a cache written here
 # carries the same signature as one the reference wrote
 _GOAL_BUILDER_VERSION = 4
-_SDF_BUILDER_VERSION = 2
-_SDF_SEMANTICS = "s4"
 MAX_SWEEPS = 1 << 20
-
-
-def _map_sig(bsp: Path) -> str:
-    """The map part of every cache signature (vision.py:275-280)."""
-    st = bsp.stat()
-    return f"v{_SDF_BUILDER_VERSION}_{st.st_size}_{st.st_mtime_ns}"
+_map_sig = vision._map_sig
 
 
 def zone_seed_box(zone, cell: float):
@@ -278,16 +271,8 @@ def build_goal_field(core, zone, cell: float, cache_dir=None, device="cuda",
     if mask_kill:
         raise NotImplementedError("kill-volume masking needs the reference's BSP hull probes; "
                                   "bake that goal field with the reference")
-    occ_file = cache / f"{bsp.stem}.slabocc_{cell:g}.npz"
-    occ_sig = f"{_map_sig(bsp)}_{_SDF_SEMANTICS}"
-    if not occ_file.exists():
-        raise FileNotFoundError(f"no occupancy cache {occ_file}: sample it once with the "
-                                "reference's slab_occupancy, or call goal_field_from_occupancy")
-    z = np.load(occ_file, allow_pickle=False)
-    if "sig" not in z or str(z["sig"]) != occ_sig:
-        raise FileNotFoundError(f"occupancy cache {occ_file} is stale (signature {occ_sig})")
-    mins = z["mins"].astype(np.float64)
-    field = goal_field_from_occupancy(z["occ"], mins, zone, cell, device=device)
+    occ, mins = vision.slab_occupancy(core, cell, cache_dir)
+    field = goal_field_from_occupancy(occ, mins, zone, cell, device=device)
     q = field.grid_q.cpu().numpy().view(np.uint16)
     np.savez_compressed(cache_file, grid=q, quant=np.float32(field.bake_info["quant"]),
                         mins=mins, cell=np.float32(cell),

@@ -27,8 +27,8 @@ import torch
 
 from . import _sdfr
 
-__all__ = ["GpuLidar", "build_sdf", "sdf_from_occupancy", "pick_cell", "grid_dims",
-           "SOLID_ENT_CLASSES"]
+__all__ = ["GpuLidar", "build_sdf", "sdf_from_occupancy", "map_occupancy", "slab_occupancy",
+           "pick_cell", "grid_dims", "SOLID_ENT_CLASSES"]
 
 # brush entities the reference's physics collides with (vision.py:301-307);
 # kept for importers of the name, the bake itself is not part of this module
@@ -39,6 +39,7 @@ SOLID_ENT_CLASSES = {"func_wall", "func_breakable", "func_pushable",
 
 _SDF_BUILDER_VERSION = 2
 _SDF_SEMANTICS = "s4"
+_OCC_SEMANTICS = "o2"
 
 _DUCK_DTYPES = {torch.float32: _sdfr.F32, torch.float16: _sdfr.F16, torch.bfloat16: _sdfr.BF16,
                 torch.int32: _sdfr.I32, torch.int64: _sdfr.I64, torch.uint8: _sdfr.U8,
@@ -73,6 +74,39 @@ def grid_dims(core, cell: float):
     return mins, nx, ny, nz
 
 
+def _map_sig(bsp: Path) -> str:
+    """The map part of every cache signature (vision.py:275-280)."""
+    st = bsp.stat()
+    return f"v{_SDF_BUILDER_VERSION}_{st.st_size}_{st.st_mtime_ns}"
+
+
+def _load_occ_cache(core, cell, cache_dir, kind: str, semantics: str):
+    bsp = Path(core.bsp_path)
+    sig = f"{_map_sig(bsp)}_{semantics}"
+    cache = Path(cache_dir) if cache_dir else bsp.parent
+    f = cache / f"{bsp.stem}.{kind}_{cell:g}.npz"
+    if f.exists():
+        z = np.load(f, allow_pickle=False)
+        if "sig" in z and str(z["sig"]) == sig:
+            return z["occ"], z["mins"].astype(np.float64)
+    raise FileNotFoundError(
+        f"no current occupancy cache at {f} (signature {sig}); sampling the map's occupancy "
+        "needs the reference's BSP core — sample it once with the reference")
+
+
+def map_occupancy(core, cell: float = 16.0, cache_dir=None):
+    """The map's voxel-centre solid occupancy, (occ uint8 [nz, ny, nx],
+    mins float64 (3,)), from the reference's cache ``<map>.occ_<cell>.npz``
+    with its signature (vision.py:325-343)."""
+    return _load_occ_cache(core, cell, cache_dir, "occ", _OCC_SEMANTICS)
+
+
+def slab_occupancy(core, cell: float = 16.0, cache_dir=None):
+    """The slab-catching occupancy the goal graph uses, from the reference's
+    cache ``<map>.slabocc_<cell>.npz`` with its signature (vision.py:346-369)."""
+    return _load_occ_cache(core, cell, cache_dir, "slabocc", _SDF_SEMANTICS)
+
+
 def build_sdf(core, cell: float = 16.0, cache_dir=None):
     """Load the map's baked distance field: (sdf [nz,ny,nx], mins (3,), cell).
 
@@ -84,8 +118,7 @@ def build_sdf(core, cell: float = 16.0, cache_dir=None):
     grid. Tests replace this function on the module, as the reference's do.
     """
     bsp = Path(core.bsp_path)
-    st = bsp.stat()
-    sig = f"v{_SDF_BUILDER_VERSION}_{st.st_size}_{st.st_mtime_ns}_{_SDF_SEMANTICS}"
+    sig = f"{_map_sig(bsp)}_{_SDF_SEMANTICS}"
     cache = Path(cache_dir) if cache_dir else bsp.parent
     f = cache / f"{bsp.stem}.sdf_{cell:g}.npz"
     if f.exists():
@@ -409,8 +442,9 @@ class GpuLidar:
         return out
 
     @torch.no_grad()
-    def ray_dirs(self, yaw_deg, pitch_deg) -> torch.Tensor:
-        """(N, H, W, 3) unit ray directions exactly as the march casts them."""
+    def ray_dirs(self, yaw_deg, pitch_deg, *, pinhole: bool | None = None) -> torch.Tensor:
+        """(N, H, W, 3) unit ray directions exactly as the march casts them
+        (``pinhole`` overrides the lidar's camera model)."""
         yaw = self._f32(yaw_deg, "yaw_deg").reshape(-1)
         pitch = self._f32(pitch_deg, "pitch_deg").reshape(-1)
         n = yaw.shape[0]
@@ -418,13 +452,47 @@ class GpuLidar:
         duck = torch.zeros(n, dtype=torch.int32, device=self.device)
         poses, keep = self._poses(zeros, yaw, pitch, duck)
         out = torch.empty(n, self.H, self.W, 3, device=self.device)
+        cam = self._cam()
+        if pinhole is not None:
+            cam.camera = _sdfr.CAM_PINHOLE if pinhole else _sdfr.CAM_EQUIANGULAR
         with torch.cuda.device(self.device):
             stream = torch.cuda.current_stream(self.device).cuda_stream
-            rc = self._lib.sdfr_ray_dirs(ctypes.byref(self._cam()), ctypes.byref(poses),
-                                         out.data_ptr(), stream)
+            rc = self._lib.sdfr_ray_dirs(ctypes.byref(cam), ctypes.byref(poses), out.data_ptr(),
+                                         stream)
         _sdfr.check(rc, "sdfr_ray_dirs", self._lib)
         del keep
         return out
+
+    # The reference's CPU path keeps ray directions in (N, H, W) buffers that
+    # its camera tests read (vision.py:531-540, :596-624; test_pinhole.py:
+    # 36-41). The same names here fill device buffers from the kernel's own
+    # ray setup.
+    def _ensure_buffers(self, N):
+        if getattr(self, "_buf_n", None) == N:
+            return
+        self._buf_n = N
+        sh = (N, self.H, self.W)
+        self._dx = torch.empty(sh, device=self.device)
+        self._dy = torch.empty(sh, device=self.device)
+        self._dz = torch.empty(sh, device=self.device)
+
+    def _dirs_into(self, N, yaw_deg, pitch_deg, d2r, pinhole):
+        if np.float32(d2r) != np.float32(np.pi / 180.0):
+            raise ValueError("the kernel converts degrees with f32(pi/180); d2r must be pi/180")
+        self._ensure_buffers(N)
+        d = self.ray_dirs(torch.as_tensor(yaw_deg).reshape(N), torch.as_tensor(pitch_deg).reshape(N),
+                          pinhole=pinhole)
+        self._dx.copy_(d[..., 0])
+        self._dy.copy_(d[..., 1])
+        self._dz.copy_(d[..., 2])
+
+    def _dirs_equiangular(self, N, yaw_deg, pitch_deg, d2r):
+        """Equiangular directions into ``_dx/_dy/_dz`` (vision.py:596-607)."""
+        self._dirs_into(N, yaw_deg, pitch_deg, d2r, False)
+
+    def _dirs_pinhole(self, N, yaw_deg, pitch_deg, d2r):
+        """Tangent-plane directions into ``_dx/_dy/_dz`` (vision.py:609-624)."""
+        self._dirs_into(N, yaw_deg, pitch_deg, d2r, True)
 
     @property
     def grid_bytes(self) -> int:

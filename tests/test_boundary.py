@@ -241,7 +241,7 @@ def test_goal_seed_box_and_cache_contract(tmp_path):
         goalfield.build_goal_field(Core(), zone, 16.0, mask_kill=True)
     np.savez(tmp_path / "surf_x.slabocc_16.npz", occ=np.zeros((2, 2, 2), np.uint8),
              mins=np.zeros(3), sig=np.str_("stale"))
-    with pytest.raises(FileNotFoundError, match="stale"):
+    with pytest.raises(FileNotFoundError, match="no current occupancy cache"):
         goalfield.build_goal_field(Core(), zone, 16.0)
     with pytest.raises(ValueError, match="no CPU path"):
         goalfield.GoalField(np.zeros((2, 2, 2), np.float32), np.zeros(3), 16.0, 10.0,
@@ -249,3 +249,31 @@ def test_goal_seed_box_and_cache_contract(tmp_path):
     with pytest.raises(ValueError, match="no CPU path"):
         goalfield.goal_field_from_occupancy(np.zeros((2, 2, 2)), np.zeros(3), zone, 16.0,
                                             device="cpu")
+
+
+def test_occupancy_caches_load_under_the_reference_signatures(tmp_path):
+    """map_occupancy / slab_occupancy read the reference's cache files
+    (vision.py:325-369): current signature -> the arrays, otherwise an error
+    (sampling needs the BSP core)."""
+    from surfgym import vision
+    bsp = tmp_path / "surf_y.bsp"
+    bsp.write_bytes(b"x" * 123)
+    st = bsp.stat()
+
+    class Core:
+        bsp_path = str(bsp)
+
+    occ = (np.arange(24).reshape(2, 3, 4) % 3 == 0).astype(np.uint8)
+    for kind, fn, sem in (("occ", vision.map_occupancy, "o2"),
+                          ("slabocc", vision.slab_occupancy, "s4")):
+        f = tmp_path / f"surf_y.{kind}_32.npz"
+        with pytest.raises(FileNotFoundError):
+            fn(Core(), 32.0)
+        np.savez_compressed(f, occ=occ, mins=np.array([1.0, 2.0, 3.0], np.float32),
+                            sig=np.str_(f"v2_{st.st_size}_{st.st_mtime_ns}_{sem}"))
+        got, mins = fn(Core(), 32.0)
+        assert np.array_equal(got, occ) and mins.dtype == np.float64
+        assert mins.tolist() == [1.0, 2.0, 3.0]
+        np.savez_compressed(f, occ=occ, mins=np.zeros(3), sig=np.str_("v2_0_0_" + sem))
+        with pytest.raises(FileNotFoundError):
+            fn(Core(), 32.0)

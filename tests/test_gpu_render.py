@@ -192,6 +192,24 @@ def test_ray_directions_equal_the_oracle(dev, W, H):
             assert np.abs(got - want).max() <= 1e-7, (pin, yaw, pitch)
 
 
+def test_reference_ray_buffer_helpers(dev):
+    """_ensure_buffers + _dirs_equiangular / _dirs_pinhole fill _dx/_dy/_dz
+    the way the reference's camera tests read them (test_pinhole.py:36-41)."""
+    W, H = 9, 5
+    w, sc = _scene("small_ramps")
+    lid = vision.GpuLidar.from_grid(sc.sdf, sc.mins, sc.cell, width=W, height=H,
+                                    grid_dtype=torch.float32, device=dev)
+    d2r = np.pi / 180.0
+    for pin, f in ((False, lid._dirs_equiangular), (True, lid._dirs_pinhole)):
+        lid._ensure_buffers(1)
+        f(1, torch.tensor([123.0]), torch.tensor([-41.0]), d2r)
+        got = torch.stack((lid._dx[0], lid._dy[0], lid._dz[0]), -1).cpu().numpy()
+        want = oracle.ray_dirs(W, H, 123.0, -41.0, pinhole=pin)
+        assert np.abs(got - want).max() <= 1e-7, pin
+    with pytest.raises(ValueError, match="pi/180"):
+        lid._dirs_equiangular(1, torch.tensor([0.0]), torch.tensor([0.0]), 1.0)
+
+
 def test_pinhole_render_matches_the_oracle(dev):
     w, sc = _scene("small_ramps")
     ps = w.poses(sc)
