@@ -34,7 +34,7 @@ extern "C" {
 
 /* Bumped on every struct or semantic change; the binding refuses a library
  * reporting another value. */
-#define SDFR_ABI_VERSION 5
+#define SDFR_ABI_VERSION 6
 
 /* Element types of caller arrays. */
 enum {
@@ -65,6 +65,14 @@ enum {
     SDFR_SCHED_PERSISTENT = 0, /* persistent waves refilling ended rays' lanes */
     SDFR_SCHED_TILES = 1,      /* default: launch-scheduled waves of 8x8 pixel tiles */
     SDFR_SCHED_SLOTS = 2       /* persistent waves of R tile slots, a drained slot takes a new tile */
+};
+
+/* The order in which the tiles schedule takes 8x8 pixel tiles. */
+enum {
+    SDFR_ORDER_LAUNCH = 0,    /* env by env, as the batch is laid out */
+    SDFR_ORDER_LOOKAHEAD = 1  /* default: sorted by where each tile's centre ray is 1.2 x near
+                                 units out (Morton order of coarse cells), so each XCD's L2
+                                 serves rays looking at one part of the map */
 };
 
 /* Grid geometry: the reference's single grid definition, grid_dims()
@@ -156,6 +164,12 @@ SDFR_API int32_t sdfr_grid_attach_surfnz(SdfrGrid* grid, const void* src, int32_
  * Surf-mask renders always use the tiles schedule. Results do not depend on any of them. No reference
  * counterpart: the Triton launch has one fixed shape (vision.py:48-54;
  * tools/proto_march.py sweeps it). */
+/* Chooses the tile order of later renders on this handle (SDFR_ORDER_*,
+ * default SDFR_ORDER_LOOKAHEAD). Applies to the tiles schedule and the
+ * surf-mask variant; results do not depend on it. Synchronous; 0 or < 0. No
+ * reference counterpart. */
+SDFR_API int32_t sdfr_grid_set_tile_order(SdfrGrid* grid, int32_t order);
+
 SDFR_API int32_t sdfr_grid_set_schedule(SdfrGrid* grid, int32_t schedule, int32_t refill_lanes,
                                         int32_t rays_per_lane);
 
@@ -163,7 +177,9 @@ SDFR_API int32_t sdfr_grid_set_schedule(SdfrGrid* grid, int32_t schedule, int32_
 SDFR_API int64_t sdfr_grid_bytes(const SdfrGrid* grid);
 
 /* Device bytes of the workspace sdfr_render needs for n_envs envs of this
- * camera: per env (W + H + 4) float2 of ray tables. < 0 on bad arguments. */
+ * camera: per env (W + H + 4) float2 of ray tables, then for the tile order
+ * one int32 and one uint16 per 8x8 tile and 2 x 4096 uint32 buckets (each
+ * part 256-byte aligned). < 0 on bad arguments. */
 SDFR_API int64_t sdfr_workspace_bytes(const SdfrCam* cam, int32_t n_envs);
 
 /* Renders N depth images: equiangular (or pinhole) rays from each env's eye,

@@ -66,6 +66,11 @@ constexpr int kCtrStride = 32;
 constexpr int kCounterWords = (kParts + 1) * kCtrStride;
 // Grids up to this size stay resident in the 256 MB Infinity Cache.
 constexpr int64_t kCacheResidentBytes = 192ll << 20;
+// Tile order: 16 cells per axis at most, Morton-numbered buckets.
+constexpr int kOrderCellsLog = 4;
+constexpr int kOrderBuckets = 1 << (3 * kOrderCellsLog);
+// Lookahead distance of the tile order, in units of the near range.
+constexpr float kOrderLookahead = 1.2f;
 
 // ---------------------------------------------------------------- errors --
 thread_local char g_err[512];
@@ -96,6 +101,7 @@ struct SdfrGrid {
     int64_t nz_bytes;
     int device;
     int cus;               // compute units of the device
+    int32_t tile_order;    // SDFR_ORDER_*: the order the tiles schedule takes tiles in
 };
 
 namespace {
@@ -222,6 +228,12 @@ struct MarchArgs {
     int refill_lanes;
     const void* nzmask;           // surf mask: |n_z|*127 int8 copy, same layout
     uint32_t nz_bytes;
+    int32_t* perm;                // tiles schedule: logical tile -> tile, or null
+    uint32_t* order_hist;         // tile-order bucket counts [kOrderBuckets], then cursors
+                                  // [kOrderBuckets] (zeroed by the ray-table kernel), or null
+    uint16_t* order_key;          // bucket of each tile
+    int order_shift;              // voxel index >> shift = tile-order cell
+    float lookahead;              // distance along the tile's centre ray that keys it
 };
 
 // Block b runs on XCD b % 8; give XCD x the x-th contiguous eighth of the
@@ -328,10 +340,129 @@ __device__ __forceinline__ void fill_axis_tables(const MarchArgs& a, uint32_t* s
 // ------------------------------------------------------------ ray tables --
 __global__ __launch_bounds__(256) void ray_tables_kernel(MarchArgs a) {
     const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    // the tile order's buckets start from zero (a kernel, not a memset, so
+    // a captured render replays correctly)
+    if (a.order_hist)
+        for (int64_t b = i; b < 2 * kOrderBuckets; b += (int64_t)gridDim.x * blockDim.x) a.order_hist[b] = 0u;
     if (i >= (int64_t)a.n_envs * a.rt_stride) return;
     const int n = (int)(i / a.rt_stride);
     const int e = (int)(i - (int64_t)n * a.rt_stride);
     a.rt[i] = table_entry(a, n, e);
+}
+
+// ------------------------------------------------------------- tile order --
+// The tiles schedule can take tiles in a spatial order instead of env order.
+// Each tile is keyed by where its centre ray is after `lookahead` units (1.2 x
+// the near range): the cell (of a grid of at most 16^3 cells over the voxel
+// grid) holding that point, numbered along a Morton curve. A counting sort by
+// key gives the permutation; the march then deals sorted tiles to XCDs in
+// contiguous runs, so each XCD's L2 serves rays that look at one part of the
+// map. Results do not depend on the order (every tile is marched exactly as
+// before); it only changes which rays share a cache. Two small kernels,
+// count and scatter, after the ray-table kernel has zeroed the buckets.
+__device__ __forceinline__ uint32_t spread_bits4(uint32_t v) {
+    v &= 15u;
+    return (v & 1u) | ((v & 2u) << 2) | ((v & 4u) << 4) | ((v & 8u) << 6);
+}
+
+template <int CAMERA>
+__device__ __forceinline__ uint32_t tile_order_key(const MarchArgs& a, int64_t tile) {
+    const int n = (int)(tile / a.tiles_per_env);
+    const int rem = (int)(tile - (int64_t)n * a.tiles_per_env);
+    const int ty = rem / a.tiles_x;
+    const int tx = rem - ty * a.tiles_x;
+    const int r = min(ty * 8 + 4, a.H - 1), c = min(tx * 8 + 4, a.W - 1);
+    const float2* rt = a.rt + (int64_t)n * a.rt_stride;
+    const float2 e01 = rt[a.H + a.W], e2 = rt[a.H + a.W + 1];
+    float2 psc = make_float2(0.f, 0.f), ysc = make_float2(0.f, 0.f);
+    if constexpr (CAMERA == SDFR_CAM_PINHOLE) {
+        psc = rt[a.H + a.W + 2];
+        ysc = rt[a.H + a.W + 3];
+    }
+    const float3 d = ray_dir<CAMERA>(rt[r], rt[a.H + c], psc, ysc);
+    const float L = a.lookahead;
+    const int ix = (int)__builtin_amdgcn_fmed3f((e01.x + d.x * L - a.mnx) * a.inv_cell, 0.0f, a.fnx1);
+    const int iy = (int)__builtin_amdgcn_fmed3f((e01.y + d.y * L - a.mny) * a.inv_cell, 0.0f, a.fny1);
+    const int iz = (int)__builtin_amdgcn_fmed3f((e2.x + d.z * L - a.mnz) * a.inv_cell, 0.0f, a.fnz1);
+    return spread_bits4((uint32_t)ix >> a.order_shift) |
+           (spread_bits4((uint32_t)iy >> a.order_shift) << 1) |
+           (spread_bits4((uint32_t)iz >> a.order_shift) << 2);
+}
+
+// Both passes give each block the same chunk of kOrderChunk tiles; buckets
+// are counted (and ranked) in LDS, so a block touches each global bucket
+// at most once per pass.
+constexpr int kOrderChunk = 1024;
+
+template <int CAMERA>
+__global__ __launch_bounds__(256) void order_count(MarchArgs a) {
+    __shared__ uint32_t h[kOrderBuckets];
+    for (int i = threadIdx.x; i < kOrderBuckets; i += blockDim.x) h[i] = 0u;
+    __syncthreads();
+    const int64_t t0 = (int64_t)blockIdx.x * kOrderChunk;
+    for (int k = threadIdx.x; k < kOrderChunk; k += blockDim.x) {
+        const int64_t t = t0 + k;
+        if (t < a.total_tiles) {
+            const uint32_t key = tile_order_key<CAMERA>(a, t);
+            a.order_key[t] = (uint16_t)key;
+            atomicAdd(&h[key], 1u);
+        }
+    }
+    __syncthreads();
+    for (int i = threadIdx.x; i < kOrderBuckets; i += blockDim.x)
+        if (h[i]) atomicAdd(&a.order_hist[i], h[i]);
+}
+
+// Each block scans the 4096 bucket counts in LDS (bucket b's first slot in
+// the sorted list), reserves a run of slots per bucket for its chunk's tiles
+// from the bucket cursors, and writes each tile into its slot.
+__global__ __launch_bounds__(256) void order_scatter(MarchArgs a) {
+    constexpr int kPer = kOrderChunk / 256;
+    constexpr int kBinsPer = kOrderBuckets / 256;
+    __shared__ uint32_t start[kOrderBuckets];  // bucket b's first slot
+    __shared__ uint32_t cnt[kOrderBuckets];    // this chunk's tiles per bucket
+    __shared__ uint32_t wave_sum[4];
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    // exclusive scan of the global counts: 16 buckets per thread
+    uint32_t v[kBinsPer], sum = 0;
+    for (int j = 0; j < kBinsPer; ++j) {
+        v[j] = a.order_hist[tid * kBinsPer + j];
+        sum += v[j];
+        cnt[tid * kBinsPer + j] = 0u;
+    }
+    uint32_t inc = sum;
+    for (int off = 1; off < 64; off <<= 1) {
+        const uint32_t o = __shfl_up(inc, off);
+        if (lane >= off) inc += o;
+    }
+    if (lane == 63) wave_sum[wv] = inc;
+    __syncthreads();
+    uint32_t run = inc - sum;
+    for (int w = 0; w < wv; ++w) run += wave_sum[w];
+    for (int j = 0; j < kBinsPer; ++j) {
+        start[tid * kBinsPer + j] = run;
+        run += v[j];
+    }
+    __syncthreads();
+    // rank this chunk's tiles within their buckets
+    const int64_t t0 = (int64_t)blockIdx.x * kOrderChunk;
+    uint32_t key[kPer], rank[kPer];
+    for (int j = 0; j < kPer; ++j) {
+        const int64_t t = t0 + tid + j * 256;
+        key[j] = t < a.total_tiles ? a.order_key[t] : 0u;
+        rank[j] = t < a.total_tiles ? atomicAdd(&cnt[key[j]], 1u) : 0u;
+    }
+    __syncthreads();
+    uint32_t* cursor = a.order_hist + kOrderBuckets;
+    for (int i = tid; i < kOrderBuckets; i += blockDim.x)
+        if (cnt[i]) start[i] += atomicAdd(&cursor[i], cnt[i]);
+    __syncthreads();
+    for (int j = 0; j < kPer; ++j) {
+        const int64_t t = t0 + tid + j * 256;
+        if (t >= a.total_tiles) continue;
+        const uint32_t pos = start[key[j]] + rank[j];
+        if ((int64_t)pos < a.total_tiles) a.perm[pos] = (int32_t)t;
+    }
 }
 
 // ------------------------------------------------------ schedule: tiles --
@@ -368,8 +499,15 @@ __global__ __launch_bounds__(256) void march_tiles(MarchArgs a) {
 #pragma unroll
     for (int j = 0; j < RPL; ++j) {
         const int64_t tile = tile0 + j;
-        const bool tile_ok = tile < a.total_tiles;
-        const int64_t tl = tile_ok ? tile : tile0;
+        bool tile_ok = tile < a.total_tiles;
+        int64_t tl = tile_ok ? tile : tile0;
+        if (a.perm) {
+            tl = a.perm[tl];
+            if (tl < 0 || tl >= a.total_tiles) {   // never for a complete permutation
+                tl = 0;
+                tile_ok = false;
+            }
+        }
         const int n = __builtin_amdgcn_readfirstlane((int)(tl / a.tiles_per_env));
         const int rem = (int)(tl - (int64_t)n * a.tiles_per_env);
         const int ty = __builtin_amdgcn_readfirstlane(rem / a.tiles_x);
@@ -845,16 +983,27 @@ void launch_slots(MarchArgs& a, const SdfrGrid* g, size_t lds, hipStream_t st) {
     }
 }
 
+template <int CAMERA>
+void launch_tile_order(const MarchArgs& a, hipStream_t st) {
+    if (!a.perm) return;
+    const int chunks = (int)((a.total_tiles + kOrderChunk - 1) / kOrderChunk);
+    order_count<CAMERA><<<chunks, 256, 0, st>>>(a);
+    order_scatter<<<chunks, 256, 0, st>>>(a);
+}
+
 template <typename GT, int LAYOUT, int OUT, int CAMERA, bool CENSUS>
 void launch_march(MarchArgs& a, const SdfrGrid* g, bool surf, hipStream_t st) {
     if (surf) {
         // the surf-mask variant exists for the equiangular camera only
         // (vision.py:463-467) and always runs the tiles schedule
-        if constexpr (CAMERA == SDFR_CAM_EQUIANGULAR)
+        if constexpr (CAMERA == SDFR_CAM_EQUIANGULAR) {
+            launch_tile_order<CAMERA>(a, st);
             launch_tiles<GT, LAYOUT, OUT, CAMERA, CENSUS, true>(a, g->rays_per_lane, st);
+        }
         return;
     }
     if (g->schedule == SDFR_SCHED_TILES) {
+        launch_tile_order<CAMERA>(a, st);
         launch_tiles<GT, LAYOUT, OUT, CAMERA, CENSUS, false>(a, g->rays_per_lane, st);
         return;
     }
@@ -955,8 +1104,19 @@ void fill_args(MarchArgs* a, const SdfrCam* cam, const SdfrPoses* poses) {
     a->rt_stride = cam->width + cam->height + 4;
 }
 
+// Render workspace: the ray tables, then the tile order's permutation and
+// buckets, each 256-byte aligned.
+int64_t align256(int64_t v) { return (v + 255) & ~(int64_t)255; }
+
+int64_t ray_table_bytes(int width, int height, int n_envs) {
+    return align256((int64_t)n_envs * (width + height + 4) * (int64_t)sizeof(float2));
+}
+
 int64_t workspace_bytes(int width, int height, int n_envs) {
-    return (int64_t)n_envs * (width + height + 4) * (int64_t)sizeof(float2);
+    const int64_t tiles = (int64_t)((width + 7) / 8) * ((height + 7) / 8) * n_envs;
+    return ray_table_bytes(width, height, n_envs) + align256(tiles * (int64_t)sizeof(int32_t)) +
+           align256(tiles * (int64_t)sizeof(uint16_t)) +
+           2 * (int64_t)kOrderBuckets * (int64_t)sizeof(uint32_t);
 }
 
 }  // namespace
@@ -1052,6 +1212,7 @@ SDFR_API SdfrGrid* sdfr_grid_create(const SdfrGridDesc* desc, const void* src, i
     // to HBM, where fewer rays in flight thrash fewer DRAM pages
     g->rays_per_lane = g->bytes > kCacheResidentBytes ? 1 : 2;
     g->cus = 0;
+    g->tile_order = SDFR_ORDER_LOOKAHEAD;
     hipError_t e = hipGetDevice(&g->device);
     if (e == hipSuccess)
         e = hipDeviceGetAttribute(&g->cus, hipDeviceAttributeMultiprocessorCount, g->device);
@@ -1150,6 +1311,15 @@ SDFR_API int32_t sdfr_grid_set_schedule(SdfrGrid* grid, int32_t schedule, int32_
     return 0;
 }
 
+SDFR_API int32_t sdfr_grid_set_tile_order(SdfrGrid* grid, int32_t order) {
+    g_err[0] = '\0';
+    if (!grid) return fail(-1, "sdfr_grid_set_tile_order: null grid handle");
+    if (order != SDFR_ORDER_LAUNCH && order != SDFR_ORDER_LOOKAHEAD)
+        return fail(-3, "sdfr_grid_set_tile_order: unknown tile order %d", order);
+    grid->tile_order = order;
+    return 0;
+}
+
 SDFR_API int32_t sdfr_render(const SdfrGrid* grid, const SdfrCam* cam, const SdfrPoses* poses,
                              const SdfrImage* image, void* workspace, int64_t workspace_size,
                              void* stream) {
@@ -1213,6 +1383,21 @@ SDFR_API int32_t sdfr_render(const SdfrGrid* grid, const SdfrCam* cam, const Sdf
     if (nblocks > 0x7fffffff)
         return fail(-2, "sdfr_render: too many envs (%lld blocks)", (long long)nblocks);
     a.nblocks = (int)nblocks;
+    a.perm = nullptr;
+    a.order_hist = nullptr;
+    a.order_key = nullptr;
+    a.order_shift = 0;
+    a.lookahead = kOrderLookahead * cam->near;
+    if (grid->tile_order == SDFR_ORDER_LOOKAHEAD && (grid->schedule == SDFR_SCHED_TILES || surf)) {
+        uint8_t* ws = (uint8_t*)workspace + ray_table_bytes(cam->width, cam->height, poses->n_envs);
+        a.perm = (int32_t*)ws;
+        ws += align256(a.total_tiles * (int64_t)sizeof(int32_t));
+        a.order_key = (uint16_t*)ws;
+        ws += align256(a.total_tiles * (int64_t)sizeof(uint16_t));
+        a.order_hist = (uint32_t*)ws;
+        const int maxdim = max(a.nx, max(a.ny, a.nz));
+        while (((maxdim - 1) >> a.order_shift) >= (1 << kOrderCellsLog)) ++a.order_shift;
+    }
 
     hipStream_t st = (hipStream_t)stream;
     const int64_t entries = (int64_t)poses->n_envs * a.rt_stride;

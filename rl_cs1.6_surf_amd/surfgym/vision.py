@@ -49,6 +49,7 @@ _OUT_DTYPES = {torch.float32: _sdfr.F32, torch.bfloat16: _sdfr.BF16}
 _LAYOUTS = {"linear": _sdfr.LAYOUT_LINEAR, "brick4": _sdfr.LAYOUT_BRICK4}
 _SCHEDULES = {"persistent": _sdfr.SCHED_PERSISTENT, "tiles": _sdfr.SCHED_TILES,
               "slots": _sdfr.SCHED_SLOTS}
+_TILE_ORDERS = {"launch": _sdfr.ORDER_LAUNCH, "lookahead": _sdfr.ORDER_LOOKAHEAD}
 
 
 def pick_cell(core, budget_voxels: float = 700e6) -> float:
@@ -194,7 +195,9 @@ class GpuLidar:
       the Infinity Cache, 1 above 192 MiB); "slots", persistent waves holding
       ``rays_per_lane`` (1-4) tiles that each take a new tile when their 64
       rays end; or "persistent" waves that refill lanes with new rays once
-      ``refill_lanes`` of them have finished. The results are identical.
+      ``refill_lanes`` of them have finished. The results are identical;
+    * ``tile_order`` — "lookahead" (default) or "launch": see
+      :meth:`set_tile_order`.
     """
 
     def __init__(self, core, width: int = 128, height: int = 64,
@@ -205,7 +208,8 @@ class GpuLidar:
                  pinhole: bool = False, *, grid_dtype=torch.float16,
                  layout: str = "brick4", hit_eps: float = None,
                  min_step: float = None, schedule: str = "tiles",
-                 refill_lanes: int = 16, rays_per_lane: int | None = None, _grid=None,
+                 refill_lanes: int = 16, rays_per_lane: int | None = None,
+                 tile_order: str = "lookahead", _grid=None,
                  _surf_nz=None) -> None:
         if surf_mask and pinhole:
             raise ValueError(
@@ -301,6 +305,7 @@ class GpuLidar:
                 rc = self._lib.sdfr_grid_attach_surfnz(h, self.snz_flat.data_ptr(), 1, stream)
             _sdfr.check(rc, "sdfr_grid_attach_surfnz", self._lib)
         self.set_schedule(schedule, refill_lanes, rays_per_lane)
+        self.set_tile_order(tile_order)
 
     def set_schedule(self, schedule: str = "tiles", refill_lanes: int = 16,
                      rays_per_lane: int | None = None) -> None:
@@ -316,6 +321,17 @@ class GpuLidar:
                     "sdfr_grid_set_schedule", self._lib)
         self.schedule, self.refill_lanes = schedule, int(refill_lanes)
         self.rays_per_lane = int(rays_per_lane)
+
+    def set_tile_order(self, order: str = "lookahead") -> None:
+        """The order the tiles schedule takes 8x8 pixel tiles in: "launch"
+        (env by env) or "lookahead" (sorted by where each tile's centre ray
+        is 1.2 x near units out, so each XCD's cache serves one part of the
+        map). Results are unchanged."""
+        if order not in _TILE_ORDERS:
+            raise ValueError(f"tile_order must be one of {sorted(_TILE_ORDERS)}, got {order!r}")
+        _sdfr.check(self._lib.sdfr_grid_set_tile_order(self._grid, _TILE_ORDERS[order]),
+                    "sdfr_grid_set_tile_order", self._lib)
+        self.tile_order = order
 
     @classmethod
     def from_grid(cls, sdf, mins, cell, surf_nz=None, **kwargs) -> "GpuLidar":

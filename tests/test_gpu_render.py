@@ -352,6 +352,53 @@ def test_schedule_arguments_are_checked(dev):
     assert (lid.schedule, lid.rays_per_lane) == ("slots", 4)
 
 
+@pytest.mark.parametrize("name,n", [("ramp_field", 256), ("winding_track", 64), ("small_ramps", 16)])
+def test_tile_order_is_a_permutation_and_changes_nothing(dev, name, n):
+    """The lookahead tile order (default) sorts the tiles; the sorted list in
+    the workspace is a permutation of all tiles, and images and censuses are
+    bit-identical to env-order launches."""
+    w, sc = _scene(name)
+    ps = w.poses(sc, n)
+    _say(f"case tile order {name} n={n}")
+    lid = _lidar(dev, w, sc)
+    assert lid.tile_order == "lookahead"
+    ta = torch.empty(n, w.height, w.width, dtype=torch.int32, device=dev)
+    a = _gpu_render(lid, ps, dev, taps=ta)
+    torch.cuda.synchronize()
+    tiles = n * (w.width // 8) * (w.height // 8)
+    rt_bytes = -(-(n * (w.width + w.height + 4) * 8) // 256) * 256
+    perm = lid._ws[rt_bytes:rt_bytes + 4 * tiles].view(torch.int32).cpu().numpy()
+    assert np.array_equal(np.sort(perm), np.arange(tiles))
+    assert not np.array_equal(perm, np.arange(tiles))       # it did reorder
+    lid.set_tile_order("launch")
+    tb = torch.empty_like(ta)
+    b = _gpu_render(lid, ps, dev, taps=tb)
+    assert torch.equal(a, b)
+    assert torch.equal(ta, tb)
+    with pytest.raises(ValueError):
+        lid.set_tile_order("zigzag")
+
+
+def test_tile_order_with_pinhole_ragged_and_surf_mask(dev):
+    w, sc = _scene("small_ramps")
+    ps = w.poses(sc, 5)
+    _say("case tile order variants")
+    o, y = torch.as_tensor(ps.origin, device=dev), torch.as_tensor(ps.yaw, device=dev)
+    p, d = torch.as_tensor(ps.pitch, device=dev), torch.as_tensor(ps.ducked, device=dev)
+    snz = np.random.default_rng(3).integers(0, 128, sc.sdf.shape).astype(np.int8)
+    for kw in (dict(pinhole=True), dict(width=37, height=19), dict(surf_nz=snz)):
+        kw.setdefault("width", w.width)
+        kw.setdefault("height", w.height)
+        lid = vision.GpuLidar.from_grid(sc.sdf, sc.mins, sc.cell, range_units=w.range_units,
+                                        near_range=w.near_range, max_steps=w.max_steps,
+                                        hit_eps=w.hit_eps, grid_dtype=torch.float32, device=dev,
+                                        **kw)
+        a = lid.render(o, y, p, d).clone()
+        lid.set_tile_order("launch")
+        b = lid.render(o, y, p, d)
+        assert torch.equal(a, b), sorted(kw)
+
+
 def test_persistent_relaunches_reuse_their_counters(dev):
     """The persistent kernel's last wave clears its tile counters: renders
     of different sizes back to back on one handle must each be complete."""
