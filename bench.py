@@ -282,6 +282,8 @@ def main(argv=None):
     ap.add_argument("--rpl", type=int, default=None,
                     help="rays per lane: tiles 1-2, slots 1-4 (default: the library's choice, "
                          "2 for cache-resident grids, 1 above 192 MiB)")
+    ap.add_argument("--tile-order", default="lookahead", choices=["lookahead", "launch"],
+                    help="order the tiles schedule takes tiles in (library default: lookahead)")
     ap.add_argument("--cpu-envs", type=int, default=2048,
                     help="envs of the workload the CPU baseline renders (default: all of ramp_field)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
@@ -324,7 +326,7 @@ def main(argv=None):
                                     max_steps=w.max_steps, hit_eps=w.hit_eps, grid_dtype=gdt,
                                     layout=args.layout, schedule=args.schedule,
                                     refill_lanes=args.refill, rays_per_lane=args.rpl,
-                                    device=dev)
+                                    tile_order=args.tile_order, device=dev)
     origin = torch.as_tensor(ps.origin, device=dev)
     yaw = torch.as_tensor(ps.yaw, device=dev)
     pitch = torch.as_tensor(ps.pitch, device=dev)
@@ -389,7 +391,8 @@ def main(argv=None):
          f"launch avg {avg_launch_ms:.4f} ms, median {med_launch_ms:.4f} ms")
 
     copy_gbs = None if args.no_copy else copy_bandwidth(dev)
-    traffic = profiled_traffic(f"{w.name} {args.schedule} rpl={lid.rays_per_lane} {args.layout} {w.store}")
+    traffic = profiled_traffic(f"{w.name} {args.schedule} rpl={lid.rays_per_lane} {args.layout} {w.store}"
+                               f" order={lid.tile_order}")
     if copy_gbs:
         _log(f"[bench] device copy {copy_gbs:.0f} GB/s")
     res = {
@@ -408,7 +411,7 @@ def main(argv=None):
         "config": {"workload": w.name, "envs": n, "image": f"{w.width}x{w.height}",
                    "rays": rays, "grid": f"{sc.nx}x{sc.ny}x{sc.nz} {w.store} @{sc.cell:g}u",
                    "layout": args.layout, "schedule": args.schedule, "refill_lanes": args.refill,
-                   "rays_per_lane": lid.rays_per_lane,
+                   "rays_per_lane": lid.rays_per_lane, "tile_order": lid.tile_order,
                    "out": w.out_dtype, "max_steps": w.max_steps,
                    "hit_eps": w.hit_eps, "range": round(w.range_units, 3),
                    "near": round(w.near_range, 3), "grid_loads_per_ray": round(loads / rays, 4),

@@ -71,6 +71,10 @@ constexpr int kOrderCellsLog = 4;
 constexpr int kOrderBuckets = 1 << (3 * kOrderCellsLog);
 // Lookahead distance of the tile order, in units of the near range.
 constexpr float kOrderLookahead = 1.2f;
+// The tile order sorts runs of this many consecutive tiles (two side by side
+// tiles of one env, a 16x8 pixel block), so the tiles one wave marches
+// together stay neighbours.
+constexpr int kOrderUnit = 2;
 
 // ---------------------------------------------------------------- errors --
 thread_local char g_err[512];
@@ -206,6 +210,7 @@ struct MarchArgs {
     uint32_t dead_off;            // gather offset for ended rays: past the range, reads 0
                                   // without touching memory
     int nx, ny, nz, bx, by, layout;
+    int grid_f16;                 // the copy stores fp16 voxels (else fp32)
     float fnx1, fny1, fnz1;       // n-1 as float: the clamp bound
     float mnx, mny, mnz, inv_cell;
     float rng, near, hit_eps, min_step;
@@ -228,12 +233,16 @@ struct MarchArgs {
     int refill_lanes;
     const void* nzmask;           // surf mask: |n_z|*127 int8 copy, same layout
     uint32_t nz_bytes;
-    int32_t* perm;                // tiles schedule: logical tile -> tile, or null
+    int32_t* perm;                // tiles schedule: logical unit -> unit, or null
     uint32_t* order_hist;         // tile-order bucket counts [kOrderBuckets], then cursors
                                   // [kOrderBuckets] (zeroed by the ray-table kernel), or null
-    uint16_t* order_key;          // bucket of each tile
+    uint16_t* order_key;          // bucket of each sorted unit
     int order_shift;              // voxel index >> shift = tile-order cell
-    float lookahead;              // distance along the tile's centre ray that keys it
+    float lookahead;              // distance along a unit's centre ray that keys it
+    int64_t order_units;          // runs of kOrderUnit tiles the order sorts
+    int64_t logical_tiles;        // tile slots the tiles schedule walks: total_tiles, or
+                                  // order_units * kOrderUnit under a tile order (a last
+                                  // partial unit leaves empty slots)
 };
 
 // Block b runs on XCD b % 8; give XCD x the x-th contiguous eighth of the
@@ -245,10 +254,28 @@ __device__ __forceinline__ int xcd_logical_block(int b, int nblocks) {
 }
 
 // -------------------------------------------------------------- ray setup --
+// The grid value every ray of an env reads at its first step: at t = 0 the
+// sample point e + d*0 is the eye itself for every direction (e + (+-0) = e
+// up to the sign of a zero, which the index formula maps to the same voxel),
+// so the whole env shares one first sample. 0 when there is no grid.
+__device__ __forceinline__ float eye_sample(const MarchArgs& a, float ex, float ey, float ez) {
+    if (!a.grid) return 0.0f;
+    const int ix = (int)__builtin_amdgcn_fmed3f((ex - a.mnx) * a.inv_cell, 0.0f, a.fnx1);
+    const int iy = (int)__builtin_amdgcn_fmed3f((ey - a.mny) * a.inv_cell, 0.0f, a.fny1);
+    const int iz = (int)__builtin_amdgcn_fmed3f((ez - a.mnz) * a.inv_cell, 0.0f, a.fnz1);
+    const int lg = a.grid_f16 ? 1 : 2;
+    const uint32_t off = axis_offset(ix, a.nx, a.ny, a.layout, a.bx, a.by, lg) +
+                         axis_offset(a.nx + iy, a.nx, a.ny, a.layout, a.bx, a.by, lg) +
+                         axis_offset(a.nx + a.ny + iz, a.nx, a.ny, a.layout, a.bx, a.by, lg);
+    const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<void*>(a.grid), 0, (int)a.grid_bytes, kRsrcWord3);
+    return a.grid_f16 ? load_voxel<__half>(rsrc, off) : load_voxel<float>(rsrc, off);
+}
+
 // Ray table of env n, entries (float2):
 //   [0, H)       rows:    equiangular (sin, cos) of pitch + poff[r];  pinhole (v[r], 0)
 //   [H, H+W)     columns: equiangular (sin, cos) of yaw + yoff[c];    pinhole (u[c], 0)
-//   H+W, H+W+1   eye: (x, y), (z, 0)
+//   H+W, H+W+1   eye: (x, y), (z, s0) with s0 the grid value at the eye voxel
 //   H+W+2, +3    pinhole only: (sin, cos) of the view pitch, of the view yaw
 // (vision.py:68-84 kernel setup; :596-624 the CPU path's _dirs_equiangular
 // and _dirs_pinhole; :499-529 the offset tables.)
@@ -268,7 +295,9 @@ __device__ __forceinline__ float2 table_entry(const MarchArgs& a, int n, int e) 
     if (e == 0) return make_float2(a.origin[n * a.origin_stride + 0], a.origin[n * a.origin_stride + 1]);
     if (e == 1) {
         const bool dk = read_ducked(a.ducked, n * a.ducked_stride, a.ducked_dtype);
-        return make_float2(a.origin[n * a.origin_stride + 2] + (dk ? 12.0f : 17.0f), 0.0f);
+        const float ez = a.origin[n * a.origin_stride + 2] + (dk ? 12.0f : 17.0f);
+        return make_float2(ez, eye_sample(a, a.origin[n * a.origin_stride + 0],
+                                          a.origin[n * a.origin_stride + 1], ez));
     }
     if (a.camera != SDFR_CAM_PINHOLE) return make_float2(0.0f, 0.0f);
     return sincos_f32(e == 2 ? pr : yr);
@@ -352,26 +381,33 @@ __global__ __launch_bounds__(256) void ray_tables_kernel(MarchArgs a) {
 
 // ------------------------------------------------------------- tile order --
 // The tiles schedule can take tiles in a spatial order instead of env order.
-// Each tile is keyed by where its centre ray is after `lookahead` units (1.2 x
+// Tiles are sorted in units of kOrderUnit consecutive tiles; each unit is
+// keyed by where its centre ray is after `lookahead` units of distance (1.2 x
 // the near range): the cell (of a grid of at most 16^3 cells over the voxel
 // grid) holding that point, numbered along a Morton curve. A counting sort by
-// key gives the permutation; the march then deals sorted tiles to XCDs in
-// contiguous runs, so each XCD's L2 serves rays that look at one part of the
-// map. Results do not depend on the order (every tile is marched exactly as
-// before); it only changes which rays share a cache. Two small kernels,
-// count and scatter, after the ray-table kernel has zeroed the buckets.
+// key gives the permutation of units; the march then deals sorted units to
+// XCDs in contiguous runs, so each XCD's L2 serves rays that look at one part
+// of the map. Results do not depend on the order (every tile is marched
+// exactly as before); it only changes which rays share a cache. Two small
+// kernels, count and scatter, after the ray-table kernel has zeroed the
+// buckets.
 __device__ __forceinline__ uint32_t spread_bits4(uint32_t v) {
     v &= 15u;
     return (v & 1u) | ((v & 2u) << 2) | ((v & 4u) << 4) | ((v & 8u) << 6);
 }
 
 template <int CAMERA>
-__device__ __forceinline__ uint32_t tile_order_key(const MarchArgs& a, int64_t tile) {
+__device__ __forceinline__ uint32_t tile_order_key(const MarchArgs& a, int64_t unit) {
+    // the unit's centre pixel: the left edge of its middle tile, or the
+    // centre of a lone last tile
+    const int64_t first = unit * kOrderUnit;
+    const bool whole = first + kOrderUnit <= a.total_tiles;
+    const int64_t tile = whole ? first + kOrderUnit / 2 : first;
     const int n = (int)(tile / a.tiles_per_env);
     const int rem = (int)(tile - (int64_t)n * a.tiles_per_env);
     const int ty = rem / a.tiles_x;
     const int tx = rem - ty * a.tiles_x;
-    const int r = min(ty * 8 + 4, a.H - 1), c = min(tx * 8 + 4, a.W - 1);
+    const int r = min(ty * 8 + 4, a.H - 1), c = min(tx * 8 + (whole ? 0 : 4), a.W - 1);
     const float2* rt = a.rt + (int64_t)n * a.rt_stride;
     const float2 e01 = rt[a.H + a.W], e2 = rt[a.H + a.W + 1];
     float2 psc = make_float2(0.f, 0.f), ysc = make_float2(0.f, 0.f);
@@ -389,7 +425,7 @@ __device__ __forceinline__ uint32_t tile_order_key(const MarchArgs& a, int64_t t
            (spread_bits4((uint32_t)iz >> a.order_shift) << 2);
 }
 
-// Both passes give each block the same chunk of kOrderChunk tiles; buckets
+// Both passes give each block the same chunk of kOrderChunk units; buckets
 // are counted (and ranked) in LDS, so a block touches each global bucket
 // at most once per pass.
 constexpr int kOrderChunk = 1024;
@@ -402,7 +438,7 @@ __global__ __launch_bounds__(256) void order_count(MarchArgs a) {
     const int64_t t0 = (int64_t)blockIdx.x * kOrderChunk;
     for (int k = threadIdx.x; k < kOrderChunk; k += blockDim.x) {
         const int64_t t = t0 + k;
-        if (t < a.total_tiles) {
+        if (t < a.order_units) {
             const uint32_t key = tile_order_key<CAMERA>(a, t);
             a.order_key[t] = (uint16_t)key;
             atomicAdd(&h[key], 1u);
@@ -414,8 +450,8 @@ __global__ __launch_bounds__(256) void order_count(MarchArgs a) {
 }
 
 // Each block scans the 4096 bucket counts in LDS (bucket b's first slot in
-// the sorted list), reserves a run of slots per bucket for its chunk's tiles
-// from the bucket cursors, and writes each tile into its slot.
+// the sorted list), reserves a run of slots per bucket for its chunk's units
+// from the bucket cursors, and writes each unit into its slot.
 __global__ __launch_bounds__(256) void order_scatter(MarchArgs a) {
     constexpr int kPer = kOrderChunk / 256;
     constexpr int kBinsPer = kOrderBuckets / 256;
@@ -444,13 +480,13 @@ __global__ __launch_bounds__(256) void order_scatter(MarchArgs a) {
         run += v[j];
     }
     __syncthreads();
-    // rank this chunk's tiles within their buckets
+    // rank this chunk's units within their buckets
     const int64_t t0 = (int64_t)blockIdx.x * kOrderChunk;
     uint32_t key[kPer], rank[kPer];
     for (int j = 0; j < kPer; ++j) {
         const int64_t t = t0 + tid + j * 256;
-        key[j] = t < a.total_tiles ? a.order_key[t] : 0u;
-        rank[j] = t < a.total_tiles ? atomicAdd(&cnt[key[j]], 1u) : 0u;
+        key[j] = t < a.order_units ? a.order_key[t] : 0u;
+        rank[j] = t < a.order_units ? atomicAdd(&cnt[key[j]], 1u) : 0u;
     }
     __syncthreads();
     uint32_t* cursor = a.order_hist + kOrderBuckets;
@@ -459,9 +495,9 @@ __global__ __launch_bounds__(256) void order_scatter(MarchArgs a) {
     __syncthreads();
     for (int j = 0; j < kPer; ++j) {
         const int64_t t = t0 + tid + j * 256;
-        if (t >= a.total_tiles) continue;
+        if (t >= a.order_units) continue;
         const uint32_t pos = start[key[j]] + rank[j];
-        if ((int64_t)pos < a.total_tiles) a.perm[pos] = (int32_t)t;
+        if ((int64_t)pos < a.order_units) a.perm[pos] = (int32_t)t;
     }
 }
 
@@ -476,7 +512,8 @@ __global__ __launch_bounds__(256) void order_scatter(MarchArgs a) {
 //
 // The step counter is wave-uniform and the loop leaves as soon as no ray of
 // the wave is alive, which is exact: alive only turns off and a dead ray adds
-// 0 to t.
+// 0 to t. Step 0 needs no gather: every ray of an env samples the eye voxel
+// first, and the ray-table pass has read that value once per env.
 //
 // SURF adds the surf-mask channel (vision.py:118-191): after the march the
 // voxel under the clamped depth is re-derived with the same index formula
@@ -490,7 +527,7 @@ __global__ __launch_bounds__(256) void march_tiles(MarchArgs a) {
     const int lane = threadIdx.x & 63;
     const int blk = xcd_logical_block(blockIdx.x, a.nblocks);
     const int64_t tile0 = ((int64_t)blk * 4 + wave) * RPL;
-    if (tile0 >= a.total_tiles) return;
+    if (tile0 >= a.logical_tiles) return;
 
     float ex[RPL], ey[RPL], ez[RPL], dx[RPL], dy[RPL], dz[RPL], t[RPL];
     int env[RPL], pix[RPL];   // env index and r*W + c of each ray
@@ -499,11 +536,14 @@ __global__ __launch_bounds__(256) void march_tiles(MarchArgs a) {
 #pragma unroll
     for (int j = 0; j < RPL; ++j) {
         const int64_t tile = tile0 + j;
-        bool tile_ok = tile < a.total_tiles;
+        bool tile_ok = tile < a.logical_tiles;
         int64_t tl = tile_ok ? tile : tile0;
         if (a.perm) {
-            tl = a.perm[tl];
-            if (tl < 0 || tl >= a.total_tiles) {   // never for a complete permutation
+            // logical tile -> (logical unit, place in it) -> sorted unit's tile
+            const int64_t ul = tl / kOrderUnit;
+            const int64_t u = a.perm[ul];
+            tl = u * kOrderUnit + (tl - ul * kOrderUnit);
+            if (u < 0 || u >= a.order_units || tl >= a.total_tiles) {   // an empty slot
                 tl = 0;
                 tile_ok = false;
             }
@@ -535,11 +575,19 @@ __global__ __launch_bounds__(256) void march_tiles(MarchArgs a) {
         alive[j] = valid[j];
         env[j] = n;
         pix[j] = rr * a.W + cc;
+        // step 0 from the env's shared eye sample (march_step at t = 0:
+        // 0 + step is the step exactly)
+        if (a.max_steps > 0 && alive[j]) {
+            const float s0 = e2.y;
+            if constexpr (CENSUS) taps[j] = 1;
+            alive[j] = (s0 > a.hit_eps) && (0.0f < a.rng);
+            if (alive[j]) t[j] = fmaxf(s0 * 0.9f, a.min_step);
+        }
     }
     const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<void*>(a.grid), 0, (int)a.grid_bytes, kRsrcWord3);
     const uint32_t* __restrict__ tab = s_axis;
-    for (int k = 0; k < a.max_steps; ++k) {
+    for (int k = 1; k < a.max_steps; ++k) {
         bool any_alive = false;
 #pragma unroll
         for (int j = 0; j < RPL; ++j) any_alive |= alive[j];
@@ -941,7 +989,7 @@ size_t axis_lds_bytes(const MarchArgs& a) {
 template <typename GT, int LAYOUT, int OUT, int CAMERA, bool CENSUS, bool SURF>
 void launch_tiles(MarchArgs& a, int rpl, hipStream_t st) {
     const size_t lds = axis_lds_bytes(a);
-    a.nblocks = (int)((a.total_tiles + 4 * rpl - 1) / (4 * rpl));
+    a.nblocks = (int)((a.logical_tiles + 4 * rpl - 1) / (4 * rpl));
     if (rpl == 2) march_tiles<GT, LAYOUT, OUT, CAMERA, CENSUS, 2, SURF><<<a.nblocks, 256, lds, st>>>(a);
     else march_tiles<GT, LAYOUT, OUT, CAMERA, CENSUS, 1, SURF><<<a.nblocks, 256, lds, st>>>(a);
 }
@@ -986,7 +1034,7 @@ void launch_slots(MarchArgs& a, const SdfrGrid* g, size_t lds, hipStream_t st) {
 template <int CAMERA>
 void launch_tile_order(const MarchArgs& a, hipStream_t st) {
     if (!a.perm) return;
-    const int chunks = (int)((a.total_tiles + kOrderChunk - 1) / kOrderChunk);
+    const int chunks = (int)((a.order_units + kOrderChunk - 1) / kOrderChunk);
     order_count<CAMERA><<<chunks, 256, 0, st>>>(a);
     order_scatter<<<chunks, 256, 0, st>>>(a);
 }
@@ -1353,6 +1401,7 @@ SDFR_API int32_t sdfr_render(const SdfrGrid* grid, const SdfrCam* cam, const Sdf
     a.rt = (float2*)workspace;
     a.grid = grid->data;
     a.grid_bytes = (uint32_t)grid->bytes;
+    a.grid_f16 = grid->store_dtype == SDFR_F16;
     // an offset at the end of the range is out of range for a 4-byte read;
     // near 4 GiB fall back to offset 0, an ordinary in-range read
     a.dead_off = grid->bytes <= 0xffffff00ll ? (uint32_t)grid->bytes : 0u;
@@ -1388,11 +1437,14 @@ SDFR_API int32_t sdfr_render(const SdfrGrid* grid, const SdfrCam* cam, const Sdf
     a.order_key = nullptr;
     a.order_shift = 0;
     a.lookahead = kOrderLookahead * cam->near;
+    a.order_units = (a.total_tiles + kOrderUnit - 1) / kOrderUnit;
+    a.logical_tiles = a.total_tiles;
     if (grid->tile_order == SDFR_ORDER_LOOKAHEAD && (grid->schedule == SDFR_SCHED_TILES || surf)) {
         uint8_t* ws = (uint8_t*)workspace + ray_table_bytes(cam->width, cam->height, poses->n_envs);
         a.perm = (int32_t*)ws;
         ws += align256(a.total_tiles * (int64_t)sizeof(int32_t));
         a.order_key = (uint16_t*)ws;
+        a.logical_tiles = a.order_units * kOrderUnit;
         ws += align256(a.total_tiles * (int64_t)sizeof(uint16_t));
         a.order_hist = (uint32_t*)ws;
         const int maxdim = max(a.nx, max(a.ny, a.nz));

@@ -354,9 +354,9 @@ def test_schedule_arguments_are_checked(dev):
 
 @pytest.mark.parametrize("name,n", [("ramp_field", 256), ("winding_track", 64), ("small_ramps", 16)])
 def test_tile_order_is_a_permutation_and_changes_nothing(dev, name, n):
-    """The lookahead tile order (default) sorts the tiles; the sorted list in
-    the workspace is a permutation of all tiles, and images and censuses are
-    bit-identical to env-order launches."""
+    """The lookahead tile order (default) sorts the tiles in runs of two; the
+    sorted list in the workspace is a permutation of all runs, and images and
+    censuses are bit-identical to env-order launches."""
     w, sc = _scene(name)
     ps = w.poses(sc, n)
     _say(f"case tile order {name} n={n}")
@@ -366,10 +366,11 @@ def test_tile_order_is_a_permutation_and_changes_nothing(dev, name, n):
     a = _gpu_render(lid, ps, dev, taps=ta)
     torch.cuda.synchronize()
     tiles = n * (w.width // 8) * (w.height // 8)
+    units = (tiles + 1) // 2
     rt_bytes = -(-(n * (w.width + w.height + 4) * 8) // 256) * 256
-    perm = lid._ws[rt_bytes:rt_bytes + 4 * tiles].view(torch.int32).cpu().numpy()
-    assert np.array_equal(np.sort(perm), np.arange(tiles))
-    assert not np.array_equal(perm, np.arange(tiles))       # it did reorder
+    perm = lid._ws[rt_bytes:rt_bytes + 4 * units].view(torch.int32).cpu().numpy()
+    assert np.array_equal(np.sort(perm), np.arange(units))
+    assert not np.array_equal(perm, np.arange(units))       # it did reorder
     lid.set_tile_order("launch")
     tb = torch.empty_like(ta)
     b = _gpu_render(lid, ps, dev, taps=tb)
@@ -386,17 +387,24 @@ def test_tile_order_with_pinhole_ragged_and_surf_mask(dev):
     o, y = torch.as_tensor(ps.origin, device=dev), torch.as_tensor(ps.yaw, device=dev)
     p, d = torch.as_tensor(ps.pitch, device=dev), torch.as_tensor(ps.ducked, device=dev)
     snz = np.random.default_rng(3).integers(0, 128, sc.sdf.shape).astype(np.int8)
-    for kw in (dict(pinhole=True), dict(width=37, height=19), dict(surf_nz=snz)):
+    # 37x19 and 8x8 over 5 envs give odd tile counts (75 and 5): the last run
+    # of the order holds one tile, and every tile must still be marched once
+    for kw in (dict(pinhole=True), dict(width=37, height=19), dict(width=8, height=8),
+               dict(width=37, height=19, rays_per_lane=1), dict(width=8, height=8, rays_per_lane=1),
+               dict(surf_nz=snz)):
         kw.setdefault("width", w.width)
         kw.setdefault("height", w.height)
         lid = vision.GpuLidar.from_grid(sc.sdf, sc.mins, sc.cell, range_units=w.range_units,
                                         near_range=w.near_range, max_steps=w.max_steps,
                                         hit_eps=w.hit_eps, grid_dtype=torch.float32, device=dev,
                                         **kw)
-        a = lid.render(o, y, p, d).clone()
+        shape = (5, kw["height"], kw["width"]) + ((2,) if "surf_nz" in kw else ())
+        a = torch.full(shape, -1.0, device=dev)   # a tile never marched stays -1
+        lid.render(o, y, p, d, out=a)
         lid.set_tile_order("launch")
         b = lid.render(o, y, p, d)
         assert torch.equal(a, b), sorted(kw)
+        assert bool((b >= 0).all()) and bool((b <= 1.25).all()), sorted(kw)
 
 
 def test_persistent_relaunches_reuse_their_counters(dev):
