@@ -34,7 +34,7 @@ extern "C" {
 
 /* Bumped on every struct or semantic change; the binding refuses a library
  * reporting another value. */
-#define SDFR_ABI_VERSION 6
+#define SDFR_ABI_VERSION 7
 
 /* Element types of caller arrays. */
 enum {
@@ -72,7 +72,8 @@ enum {
     SDFR_ORDER_LAUNCH = 0,    /* env by env, as the batch is laid out */
     SDFR_ORDER_LOOKAHEAD = 1  /* default: sorted by where each tile's centre ray is 1.2 x near
                                  units out (Morton order of coarse cells), so each XCD's L2
-                                 serves rays looking at one part of the map */
+                                 serves rays looking at one part of the map; applied to
+                                 renders of at least min_tiles tiles */
 };
 
 /* Grid geometry: the reference's single grid definition, grid_dims()
@@ -161,17 +162,21 @@ SDFR_API int32_t sdfr_grid_attach_surfnz(SdfrGrid* grid, const void* src, int32_
  * default 16) is the number of free lanes at which a persistent wave takes
  * new rays; `rays_per_lane` is how many tiles a wave marches at once: 1 or
  * 2 (default 2) for the tiles schedule, 1..4 slots for the slots schedule.
- * Surf-mask renders always use the tiles schedule. Results do not depend on any of them. No reference
- * counterpart: the Triton launch has one fixed shape (vision.py:48-54;
- * tools/proto_march.py sweeps it). */
-/* Chooses the tile order of later renders on this handle (SDFR_ORDER_*,
- * default SDFR_ORDER_LOOKAHEAD). Applies to the tiles schedule and the
- * surf-mask variant; results do not depend on it. Synchronous; 0 or < 0. No
- * reference counterpart. */
-SDFR_API int32_t sdfr_grid_set_tile_order(SdfrGrid* grid, int32_t order);
-
+ * Surf-mask renders always use the tiles schedule. Results do not depend
+ * on any of them. Synchronous; 0 or < 0. No reference counterpart: the
+ * Triton launch has one fixed shape (vision.py:48-54; tools/proto_march.py
+ * sweeps it). */
 SDFR_API int32_t sdfr_grid_set_schedule(SdfrGrid* grid, int32_t schedule, int32_t refill_lanes,
                                         int32_t rays_per_lane);
+
+/* Chooses the tile order of later renders on this handle (SDFR_ORDER_*,
+ * default SDFR_ORDER_LOOKAHEAD). The lookahead order costs two small sort
+ * launches per render, so it applies only to renders of at least
+ * `min_tiles` 8x8 tiles (< 0: the library default, 65536 = 512 envs of
+ * 128x64; 0: always); smaller renders take the launch order. Applies to the
+ * tiles schedule and the surf-mask variant; results do not depend on it.
+ * Synchronous; 0 or < 0. No reference counterpart. */
+SDFR_API int32_t sdfr_grid_set_tile_order(SdfrGrid* grid, int32_t order, int64_t min_tiles);
 
 /* Bytes of device memory the handle owns (the re-laid-out grid). */
 SDFR_API int64_t sdfr_grid_bytes(const SdfrGrid* grid);

@@ -23,22 +23,26 @@
 // are evaluated in fp64 and rounded once to fp32, which gives the correctly
 // rounded fp32 value except in cases rarer than 1 in 2^28.
 //
-// One render is two launches on the caller's stream:
+// One render is two to four launches on the caller's stream:
 //   1. ray_tables: per env, the (sin, cos) of its H row pitch angles and W
 //      column yaw angles, and its eye point — all the transcendental work of
 //      ray setup, (H+W) fp64 sincos per env instead of two per ray;
-//   2. the march, in one of two schedules with identical results:
-//      - tiles (default): launch-scheduled waves, each marching 8x8 pixel
-//        tiles with RPL rays per lane in flight at once;
+//   2. (tiles schedule, lookahead order) order_count + order_scatter: a
+//      counting sort of the tiles by where they look (see "tile order");
+//   3. the march, in one of three schedules with identical results:
+//      - tiles (default): launch-scheduled two-wave workgroups, each wave
+//        marching 8x8 pixel tiles with RPL rays per lane in flight at once;
 //      - persistent: a grid that fills the GPU once; each wave keeps 64 ray
 //        slots and refills finished slots with new rays (ray compaction),
 //        pulling 8x8 pixel tiles from per-XCD work counters. It keeps every
 //        lane busy but mixes rays of different depths in one gather, which
 //        costs more cache lines per gather than it saves in idle lanes on
-//        the scenes measured so far, so it is not the default.
-// Blocks are numbered so that each XCD (blocks are dealt to the 8 XCDs
-// round-robin) works on a contiguous run of envs, keeping an env's rays in
-// one L2.
+//        the scenes measured so far, so it is not the default;
+//      - slots: persistent waves of R tile slots (see march_slots).
+// Blocks are dealt to the 8 XCDs round-robin by the hardware; they are
+// numbered so that each XCD works on a contiguous run of envs (env order), or
+// on interleaved chunks of the sorted tile list (lookahead order), keeping
+// rays that share grid data in one L2.
 
 #include <hip/hip_runtime.h>
 #include <hip/hip_fp16.h>
@@ -71,10 +75,21 @@ constexpr int kOrderCellsLog = 4;
 constexpr int kOrderBuckets = 1 << (3 * kOrderCellsLog);
 // Lookahead distance of the tile order, in units of the near range.
 constexpr float kOrderLookahead = 1.2f;
-// The tile order sorts runs of this many consecutive tiles (two side by side
-// tiles of one env, a 16x8 pixel block), so the tiles one wave marches
-// together stay neighbours.
-constexpr int kOrderUnit = 2;
+// Renders of fewer tiles skip the sort by default: its two launches cost
+// ~9 us, more than it saves below ~512 envs of 128x64.
+constexpr int64_t kOrderMinTiles = 1 << 16;
+// Waves per workgroup of the tiles schedule. A workgroup's slot on the CU is
+// freed only when its slowest wave ends, so small workgroups waste fewer
+// wave slots on the long-ray tail; two (rather than one) keep the per-
+// workgroup LDS axis tables within the CU's LDS at full occupancy on the
+// largest grids.
+constexpr int kTileWaves = 2;
+// Sorted tile-order blocks are dealt to the XCDs in chunks of this many
+// workgroups: XCD x takes chunks x, x+8, x+16, ... A chunk keeps one XCD's
+// concurrent rays in one part of the map, and interleaving the chunks
+// spreads cheap regions (sky) and costly ones (grazing ground) evenly over
+// the XCDs, which a contiguous eighth per XCD does not.
+constexpr int kXcdChunk = 64;
 
 // ---------------------------------------------------------------- errors --
 thread_local char g_err[512];
@@ -106,6 +121,7 @@ struct SdfrGrid {
     int device;
     int cus;               // compute units of the device
     int32_t tile_order;    // SDFR_ORDER_*: the order the tiles schedule takes tiles in
+    int64_t order_min_tiles;  // ... applied to renders of at least this many tiles
 };
 
 namespace {
@@ -239,9 +255,10 @@ struct MarchArgs {
     uint16_t* order_key;          // bucket of each sorted unit
     int order_shift;              // voxel index >> shift = tile-order cell
     float lookahead;              // distance along a unit's centre ray that keys it
-    int64_t order_units;          // runs of kOrderUnit tiles the order sorts
+    int order_unit;               // tiles per sorted unit: one workgroup's, kTileWaves * RPL
+    int64_t order_units;          // units the order sorts
     int64_t logical_tiles;        // tile slots the tiles schedule walks: total_tiles, or
-                                  // order_units * kOrderUnit under a tile order (a last
+                                  // order_units * order_unit under a tile order (a last
                                   // partial unit leaves empty slots)
 };
 
@@ -251,6 +268,18 @@ __device__ __forceinline__ int xcd_logical_block(int b, int nblocks) {
     int q = nblocks >> 3, rem = nblocks & 7;
     int x = b & 7, i = b >> 3;
     return x * q + (x < rem ? x : rem) + i;
+}
+
+// Block b runs on XCD x = b % 8 as that XCD's i-th block (i = b / 8); give
+// it logical block ((i / C) * 8 + x) * C + i % C, so XCD x walks chunks x,
+// x+8, x+16, ... of C logical blocks. The blocks beyond the last whole round
+// of 8 chunks map to themselves (a bijection for any block count).
+__device__ __forceinline__ int xcd_chunked_block(int b, int nblocks, int C) {
+    const int full = (nblocks / (8 * C)) * 8 * C;
+    if (b >= full) return b;
+    const int i = b >> 3, x = b & 7;
+    const int k = i / C, o = i - k * C;
+    return (k * 8 + x) * C + o;
 }
 
 // -------------------------------------------------------------- ray setup --
@@ -381,16 +410,18 @@ __global__ __launch_bounds__(256) void ray_tables_kernel(MarchArgs a) {
 
 // ------------------------------------------------------------- tile order --
 // The tiles schedule can take tiles in a spatial order instead of env order.
-// Tiles are sorted in units of kOrderUnit consecutive tiles; each unit is
-// keyed by where its centre ray is after `lookahead` units of distance (1.2 x
-// the near range): the cell (of a grid of at most 16^3 cells over the voxel
+// Tiles are sorted in units of one workgroup's tiles (kTileWaves * RPL
+// consecutive tiles, side by side in one image row of one env, so the waves
+// of a workgroup march similar rays and end together); each unit is keyed by
+// where its centre ray is after `lookahead` units of distance (1.2 x the
+// near range): the cell (of a grid of at most 16^3 cells over the voxel
 // grid) holding that point, numbered along a Morton curve. A counting sort by
-// key gives the permutation of units; the march then deals sorted units to
-// XCDs in contiguous runs, so each XCD's L2 serves rays that look at one part
-// of the map. Results do not depend on the order (every tile is marched
-// exactly as before); it only changes which rays share a cache. Two small
-// kernels, count and scatter, after the ray-table kernel has zeroed the
-// buckets.
+// key gives the permutation of units; the march then deals chunks of the
+// sorted list to the XCDs (xcd_chunked_block), so at any time each XCD's L2
+// serves rays that look at one part of the map. Results do not depend on the
+// order (every tile is marched exactly as before); it only changes which
+// rays share a cache. Two small kernels, count and scatter, after the
+// ray-table kernel has zeroed the buckets.
 __device__ __forceinline__ uint32_t spread_bits4(uint32_t v) {
     v &= 15u;
     return (v & 1u) | ((v & 2u) << 2) | ((v & 4u) << 4) | ((v & 8u) << 6);
@@ -400,9 +431,9 @@ template <int CAMERA>
 __device__ __forceinline__ uint32_t tile_order_key(const MarchArgs& a, int64_t unit) {
     // the unit's centre pixel: the left edge of its middle tile, or the
     // centre of a lone last tile
-    const int64_t first = unit * kOrderUnit;
-    const bool whole = first + kOrderUnit <= a.total_tiles;
-    const int64_t tile = whole ? first + kOrderUnit / 2 : first;
+    const int64_t first = unit * a.order_unit;
+    const bool whole = first + a.order_unit <= a.total_tiles;
+    const int64_t tile = whole ? first + a.order_unit / 2 : first;
     const int n = (int)(tile / a.tiles_per_env);
     const int rem = (int)(tile - (int64_t)n * a.tiles_per_env);
     const int ty = rem / a.tiles_x;
@@ -502,9 +533,9 @@ __global__ __launch_bounds__(256) void order_scatter(MarchArgs a) {
 }
 
 // ------------------------------------------------------ schedule: tiles --
-// Each wave64 marches RPL 8x8 pixel tiles of consecutive tile index (so,
-// mostly, neighbouring tiles of one env): lane l holds pixel l of every one
-// of them. Per step a lane issues the gathers of all its live rays before
+// Workgroups of kTileWaves waves. Each wave64 marches RPL 8x8 pixel tiles of
+// consecutive tile index (so, mostly, neighbouring tiles of one env): lane l
+// holds pixel l of every one of them. Per step a lane issues the gathers of all its live rays before
 // using any, so RPL independent loads per lane are in flight at once — the
 // march is bound by gather latency, and this multiplies the loads in flight
 // without more waves. Lanes of dead rays point their load past the end of
@@ -520,13 +551,14 @@ __global__ __launch_bounds__(256) void order_scatter(MarchArgs a) {
 // and the |n_z| grid (int8, |n_z|*127) is read there; the image is then
 // interleaved (depth, |n_z|) per pixel, channel fastest (vision.py:558-570).
 template <typename GT, int LAYOUT, int OUT_DTYPE, int CAMERA, bool CENSUS, int RPL, bool SURF>
-__global__ __launch_bounds__(256) void march_tiles(MarchArgs a) {
+__global__ __launch_bounds__(64 * kTileWaves) void march_tiles(MarchArgs a) {
     extern __shared__ uint32_t s_axis[];
     fill_axis_tables<GT, LAYOUT>(a, s_axis);
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int lane = threadIdx.x & 63;
-    const int blk = xcd_logical_block(blockIdx.x, a.nblocks);
-    const int64_t tile0 = ((int64_t)blk * 4 + wave) * RPL;
+    const int blk = a.perm ? xcd_chunked_block(blockIdx.x, a.nblocks, kXcdChunk)
+                           : xcd_logical_block(blockIdx.x, a.nblocks);
+    const int64_t tile0 = ((int64_t)blk * kTileWaves + wave) * RPL;
     if (tile0 >= a.logical_tiles) return;
 
     float ex[RPL], ey[RPL], ez[RPL], dx[RPL], dy[RPL], dz[RPL], t[RPL];
@@ -540,9 +572,9 @@ __global__ __launch_bounds__(256) void march_tiles(MarchArgs a) {
         int64_t tl = tile_ok ? tile : tile0;
         if (a.perm) {
             // logical tile -> (logical unit, place in it) -> sorted unit's tile
-            const int64_t ul = tl / kOrderUnit;
+            const int64_t ul = tl / a.order_unit;
             const int64_t u = a.perm[ul];
-            tl = u * kOrderUnit + (tl - ul * kOrderUnit);
+            tl = u * a.order_unit + (tl - ul * a.order_unit);
             if (u < 0 || u >= a.order_units || tl >= a.total_tiles) {   // an empty slot
                 tl = 0;
                 tile_ok = false;
@@ -989,9 +1021,12 @@ size_t axis_lds_bytes(const MarchArgs& a) {
 template <typename GT, int LAYOUT, int OUT, int CAMERA, bool CENSUS, bool SURF>
 void launch_tiles(MarchArgs& a, int rpl, hipStream_t st) {
     const size_t lds = axis_lds_bytes(a);
-    a.nblocks = (int)((a.logical_tiles + 4 * rpl - 1) / (4 * rpl));
-    if (rpl == 2) march_tiles<GT, LAYOUT, OUT, CAMERA, CENSUS, 2, SURF><<<a.nblocks, 256, lds, st>>>(a);
-    else march_tiles<GT, LAYOUT, OUT, CAMERA, CENSUS, 1, SURF><<<a.nblocks, 256, lds, st>>>(a);
+    const int per_block = kTileWaves * rpl;
+    a.nblocks = (int)((a.logical_tiles + per_block - 1) / per_block);
+    if (rpl == 2)
+        march_tiles<GT, LAYOUT, OUT, CAMERA, CENSUS, 2, SURF><<<a.nblocks, 64 * kTileWaves, lds, st>>>(a);
+    else
+        march_tiles<GT, LAYOUT, OUT, CAMERA, CENSUS, 1, SURF><<<a.nblocks, 64 * kTileWaves, lds, st>>>(a);
 }
 
 // A grid that fills every CU once (never more waves than tiles) for a
@@ -1261,6 +1296,7 @@ SDFR_API SdfrGrid* sdfr_grid_create(const SdfrGridDesc* desc, const void* src, i
     g->rays_per_lane = g->bytes > kCacheResidentBytes ? 1 : 2;
     g->cus = 0;
     g->tile_order = SDFR_ORDER_LOOKAHEAD;
+    g->order_min_tiles = kOrderMinTiles;
     hipError_t e = hipGetDevice(&g->device);
     if (e == hipSuccess)
         e = hipDeviceGetAttribute(&g->cus, hipDeviceAttributeMultiprocessorCount, g->device);
@@ -1359,12 +1395,13 @@ SDFR_API int32_t sdfr_grid_set_schedule(SdfrGrid* grid, int32_t schedule, int32_
     return 0;
 }
 
-SDFR_API int32_t sdfr_grid_set_tile_order(SdfrGrid* grid, int32_t order) {
+SDFR_API int32_t sdfr_grid_set_tile_order(SdfrGrid* grid, int32_t order, int64_t min_tiles) {
     g_err[0] = '\0';
     if (!grid) return fail(-1, "sdfr_grid_set_tile_order: null grid handle");
     if (order != SDFR_ORDER_LAUNCH && order != SDFR_ORDER_LOOKAHEAD)
         return fail(-3, "sdfr_grid_set_tile_order: unknown tile order %d", order);
     grid->tile_order = order;
+    grid->order_min_tiles = min_tiles < 0 ? kOrderMinTiles : min_tiles;
     return 0;
 }
 
@@ -1428,7 +1465,7 @@ SDFR_API int32_t sdfr_render(const SdfrGrid* grid, const SdfrCam* cam, const Sdf
     a.tiles_x = (cam->width + 7) / 8;
     a.tiles_per_env = a.tiles_x * ((cam->height + 7) / 8);
     a.total_tiles = (int64_t)a.tiles_per_env * poses->n_envs;
-    const int64_t nblocks = (a.total_tiles + 3) / 4;
+    const int64_t nblocks = (a.total_tiles + kTileWaves - 1) / kTileWaves;
     if (nblocks > 0x7fffffff)
         return fail(-2, "sdfr_render: too many envs (%lld blocks)", (long long)nblocks);
     a.nblocks = (int)nblocks;
@@ -1437,14 +1474,16 @@ SDFR_API int32_t sdfr_render(const SdfrGrid* grid, const SdfrCam* cam, const Sdf
     a.order_key = nullptr;
     a.order_shift = 0;
     a.lookahead = kOrderLookahead * cam->near;
-    a.order_units = (a.total_tiles + kOrderUnit - 1) / kOrderUnit;
+    a.order_unit = kTileWaves * grid->rays_per_lane;
+    a.order_units = (a.total_tiles + a.order_unit - 1) / a.order_unit;
     a.logical_tiles = a.total_tiles;
-    if (grid->tile_order == SDFR_ORDER_LOOKAHEAD && (grid->schedule == SDFR_SCHED_TILES || surf)) {
+    if (grid->tile_order == SDFR_ORDER_LOOKAHEAD && (grid->schedule == SDFR_SCHED_TILES || surf) &&
+        a.total_tiles >= grid->order_min_tiles) {
         uint8_t* ws = (uint8_t*)workspace + ray_table_bytes(cam->width, cam->height, poses->n_envs);
         a.perm = (int32_t*)ws;
         ws += align256(a.total_tiles * (int64_t)sizeof(int32_t));
         a.order_key = (uint16_t*)ws;
-        a.logical_tiles = a.order_units * kOrderUnit;
+        a.logical_tiles = a.order_units * a.order_unit;
         ws += align256(a.total_tiles * (int64_t)sizeof(uint16_t));
         a.order_hist = (uint32_t*)ws;
         const int maxdim = max(a.nx, max(a.ny, a.nz));

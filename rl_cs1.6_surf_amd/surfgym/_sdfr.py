@@ -18,7 +18,7 @@ import torch  # noqa: F401  (load torch's HIP runtime first, see above)
 PKG_ROOT = Path(__file__).resolve().parents[1]
 LIB_PATH = PKG_ROOT / "lib" / "libsdfr.so"
 
-ABI_VERSION = 6
+ABI_VERSION = 7
 
 # element types (SDFR_* in sdfr.h)
 F32, F16, BF16, I32, I64, U8, F64, U16 = 0, 1, 2, 3, 4, 5, 6, 7
@@ -103,7 +103,7 @@ def load(path: Path | str | None = None):
     lib.sdfr_grid_set_schedule.restype = i32
     lib.sdfr_grid_set_schedule.argtypes = [vp, i32, i32, i32]
     lib.sdfr_grid_set_tile_order.restype = i32
-    lib.sdfr_grid_set_tile_order.argtypes = [vp, i32]
+    lib.sdfr_grid_set_tile_order.argtypes = [vp, i32, i64]
     lib.sdfr_workspace_bytes.restype = i64
     lib.sdfr_workspace_bytes.argtypes = [ctypes.POINTER(Cam), i32]
     lib.sdfr_render.restype = i32

@@ -322,14 +322,20 @@ class GpuLidar:
         self.schedule, self.refill_lanes = schedule, int(refill_lanes)
         self.rays_per_lane = int(rays_per_lane)
 
-    def set_tile_order(self, order: str = "lookahead") -> None:
+    def set_tile_order(self, order: str = "lookahead", min_tiles: int | None = None) -> None:
         """The order the tiles schedule takes 8x8 pixel tiles in: "launch"
         (env by env) or "lookahead" (sorted by where each tile's centre ray
         is 1.2 x near units out, so each XCD's cache serves one part of the
-        map). Results are unchanged."""
+        map). The sort costs two small launches, so "lookahead" applies to
+        renders of at least ``min_tiles`` tiles (None: the library's
+        default, 65536 = 512 envs of 128x64; 0: always). Results are
+        unchanged."""
         if order not in _TILE_ORDERS:
             raise ValueError(f"tile_order must be one of {sorted(_TILE_ORDERS)}, got {order!r}")
-        _sdfr.check(self._lib.sdfr_grid_set_tile_order(self._grid, _TILE_ORDERS[order]),
+        mt = -1 if min_tiles is None else int(min_tiles)
+        if min_tiles is not None and mt < 0:
+            raise ValueError(f"min_tiles must be >= 0, got {min_tiles}")
+        _sdfr.check(self._lib.sdfr_grid_set_tile_order(self._grid, _TILE_ORDERS[order], mt),
                     "sdfr_grid_set_tile_order", self._lib)
         self.tile_order = order
 

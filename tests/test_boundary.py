@@ -97,6 +97,15 @@ def test_grid_create_rejects_bad_descriptors_without_a_device():
     assert b"null" in err.value
 
 
+def test_schedule_and_tile_order_reject_a_null_handle_without_a_device():
+    from surfgym import _sdfr
+    lib = _sdfr.load()
+    assert lib.sdfr_grid_set_tile_order(None, _sdfr.ORDER_LOOKAHEAD, -1) == -1
+    assert "null grid" in _sdfr.last_error()
+    assert lib.sdfr_grid_set_schedule(None, _sdfr.SCHED_TILES, 16, 2) == -1
+    assert "null grid" in _sdfr.last_error()
+
+
 def test_render_rejects_bad_arguments_without_a_device():
     from surfgym import _sdfr
     lib = _sdfr.load()

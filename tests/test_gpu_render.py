@@ -354,19 +354,24 @@ def test_schedule_arguments_are_checked(dev):
 
 @pytest.mark.parametrize("name,n", [("ramp_field", 256), ("winding_track", 64), ("small_ramps", 16)])
 def test_tile_order_is_a_permutation_and_changes_nothing(dev, name, n):
-    """The lookahead tile order (default) sorts the tiles in runs of two; the
-    sorted list in the workspace is a permutation of all runs, and images and
-    censuses are bit-identical to env-order launches."""
+    """The lookahead tile order (default) sorts the tiles in runs of one
+    workgroup's tiles (two waves x rays per lane); the sorted list in the
+    workspace is a permutation of all runs, and images and censuses are
+    bit-identical to env-order launches."""
     w, sc = _scene(name)
     ps = w.poses(sc, n)
     _say(f"case tile order {name} n={n}")
     lid = _lidar(dev, w, sc)
     assert lid.tile_order == "lookahead"
-    ta = torch.empty(n, w.height, w.width, dtype=torch.int32, device=dev)
-    a = _gpu_render(lid, ps, dev, taps=ta)
+    lid.set_tile_order("lookahead", min_tiles=0)      # sort however small the render
+    # a tile the sorted schedule never marched would keep these fills
+    ta = torch.full((n, w.height, w.width), -1, dtype=torch.int32, device=dev)
+    a = torch.full((n, w.height, w.width), -1.0, device=dev)
+    _gpu_render(lid, ps, dev, taps=ta, out=a)
     torch.cuda.synchronize()
     tiles = n * (w.width // 8) * (w.height // 8)
-    units = (tiles + 1) // 2
+    unit = 2 * lid.rays_per_lane
+    units = (tiles + unit - 1) // unit
     rt_bytes = -(-(n * (w.width + w.height + 4) * 8) // 256) * 256
     perm = lid._ws[rt_bytes:rt_bytes + 4 * units].view(torch.int32).cpu().numpy()
     assert np.array_equal(np.sort(perm), np.arange(units))
@@ -378,6 +383,30 @@ def test_tile_order_is_a_permutation_and_changes_nothing(dev, name, n):
     assert torch.equal(ta, tb)
     with pytest.raises(ValueError):
         lid.set_tile_order("zigzag")
+    with pytest.raises(ValueError):
+        lid.set_tile_order("lookahead", min_tiles=-2)
+
+
+def test_small_renders_skip_the_sort_by_default(dev):
+    """Below 65536 tiles the lookahead order leaves the sort out (its two
+    launches cost more than they save); min_tiles moves the threshold."""
+    w, sc = _scene("small_ramps")
+    n = 16
+    ps = w.poses(sc, n)
+    _say("case tile order threshold")
+    lid = _lidar(dev, w, sc)
+    tiles = n * (w.width // 8) * (w.height // 8)
+    rt_bytes = -(-(n * (w.width + w.height + 4) * 8) // 256) * 256
+    want = _gpu_render(lid, ps, dev).clone()
+    units = tiles // (2 * lid.rays_per_lane)
+    for min_tiles, sorted_ in ((None, False), (tiles + 1, False), (tiles, True), (0, True)):
+        lid.set_tile_order("lookahead", min_tiles=min_tiles)
+        lid._ws[rt_bytes:rt_bytes + 4 * units].fill_(255)       # perm slots read -1
+        got = _gpu_render(lid, ps, dev)
+        torch.cuda.synchronize()
+        perm = lid._ws[rt_bytes:rt_bytes + 4 * units].view(torch.int32).cpu().numpy()
+        assert torch.equal(got, want), min_tiles
+        assert bool((perm >= 0).all()) == sorted_, min_tiles
 
 
 def test_tile_order_with_pinhole_ragged_and_surf_mask(dev):
@@ -399,6 +428,7 @@ def test_tile_order_with_pinhole_ragged_and_surf_mask(dev):
                                         hit_eps=w.hit_eps, grid_dtype=torch.float32, device=dev,
                                         **kw)
         shape = (5, kw["height"], kw["width"]) + ((2,) if "surf_nz" in kw else ())
+        lid.set_tile_order("lookahead", min_tiles=0)
         a = torch.full(shape, -1.0, device=dev)   # a tile never marched stays -1
         lid.render(o, y, p, d, out=a)
         lid.set_tile_order("launch")
