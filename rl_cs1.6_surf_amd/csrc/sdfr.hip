@@ -619,30 +619,45 @@ __global__ __launch_bounds__(64 * kTileWaves) void march_tiles(MarchArgs a) {
     const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<void*>(a.grid), 0, (int)a.grid_bytes, kRsrcWord3);
     const uint32_t* __restrict__ tab = s_axis;
-    for (int k = 1; k < a.max_steps; ++k) {
-        bool any_alive = false;
+    // Liveness is kept as one 64-bit lane mask per tile (scalar registers):
+    // a new mask is the old one ANDed with the ballots of the two compares,
+    // and inverse_ballot turns it back into the per-lane predicate, so no
+    // vector instruction is spent on bookkeeping. A tile whose rays have all
+    // ended skips its address math and gather.
+    uint64_t live[RPL];
 #pragma unroll
-        for (int j = 0; j < RPL; ++j) any_alive |= alive[j];
-        if (!__any(any_alive)) break;
+    for (int j = 0; j < RPL; ++j) live[j] = __builtin_amdgcn_ballot_w64(alive[j]);
+    for (int k = 1; k < a.max_steps; ++k) {
+        uint64_t any = 0;
+#pragma unroll
+        for (int j = 0; j < RPL; ++j) any |= live[j];
+        if (any == 0) break;
         float sd[RPL];
 #pragma unroll
         for (int j = 0; j < RPL; ++j) {
-            const float px = ex[j] + dx[j] * t[j];
-            const float py = ey[j] + dy[j] * t[j];
-            const float pz = ez[j] + dz[j] * t[j];
-            const int ix = (int)__builtin_amdgcn_fmed3f((px - a.mnx) * a.inv_cell, 0.0f, a.fnx1);
-            const int iy = (int)__builtin_amdgcn_fmed3f((py - a.mny) * a.inv_cell, 0.0f, a.fny1);
-            const int iz = (int)__builtin_amdgcn_fmed3f((pz - a.mnz) * a.inv_cell, 0.0f, a.fnz1);
-            const uint32_t off = alive[j] ? tab[ix] + tab[a.nx + iy] + tab[a.nx + a.ny + iz] : a.dead_off;
-            sd[j] = load_voxel<GT>(rsrc, off);
+            float s = 0.0f;
+            if (live[j] != 0) {
+                const bool l = __builtin_amdgcn_inverse_ballot_w64(live[j]);
+                const float px = ex[j] + dx[j] * t[j];
+                const float py = ey[j] + dy[j] * t[j];
+                const float pz = ez[j] + dz[j] * t[j];
+                const int ix = (int)__builtin_amdgcn_fmed3f((px - a.mnx) * a.inv_cell, 0.0f, a.fnx1);
+                const int iy = (int)__builtin_amdgcn_fmed3f((py - a.mny) * a.inv_cell, 0.0f, a.fny1);
+                const int iz = (int)__builtin_amdgcn_fmed3f((pz - a.mnz) * a.inv_cell, 0.0f, a.fnz1);
+                const uint32_t off = l ? tab[ix] + tab[a.nx + iy] + tab[a.nx + a.ny + iz] : a.dead_off;
+                s = load_voxel<GT>(rsrc, off);
+            }
+            sd[j] = s;
         }
 #pragma unroll
         for (int j = 0; j < RPL; ++j) {
-            if (alive[j]) {
-                if constexpr (CENSUS) ++taps[j];
-                alive[j] = (sd[j] > a.hit_eps) && (t[j] < a.rng);
-                if (alive[j]) t[j] = t[j] + fmaxf(sd[j] * 0.9f, a.min_step);
-            }
+            if constexpr (CENSUS) taps[j] += __builtin_amdgcn_inverse_ballot_w64(live[j]) ? 1 : 0;
+            // alive = alive && s > hit_eps && t < range (vision.py:109); an
+            // ended lane's bit stays 0 whatever its compares say
+            live[j] &= __builtin_amdgcn_ballot_w64(sd[j] > a.hit_eps) &
+                       __builtin_amdgcn_ballot_w64(t[j] < a.rng);
+            const float tn = t[j] + fmaxf(sd[j] * 0.9f, a.min_step);
+            t[j] = __builtin_amdgcn_inverse_ballot_w64(live[j]) ? tn : t[j];
         }
     }
     constexpr int CH = SURF ? 2 : 1;
