@@ -223,8 +223,8 @@ __device__ __forceinline__ float2 sincos_f32(float x) {
 struct MarchArgs {
     const void* grid;
     uint32_t grid_bytes;          // size of the device copy (the descriptor's range)
-    uint32_t dead_off;            // gather offset for ended rays: past the range, reads 0
-                                  // without touching memory
+    uint32_t dead_off;            // slots and persistent schedules: gather offset for ended
+                                  // rays, past the range (reads 0 without touching memory)
     int nx, ny, nz, bx, by, layout;
     int grid_f16;                 // the copy stores fp16 voxels (else fp32)
     float fnx1, fny1, fnz1;       // n-1 as float: the clamp bound
@@ -535,11 +535,10 @@ __global__ __launch_bounds__(256) void order_scatter(MarchArgs a) {
 // ------------------------------------------------------ schedule: tiles --
 // Workgroups of kTileWaves waves. Each wave64 marches RPL 8x8 pixel tiles of
 // consecutive tile index (so, mostly, neighbouring tiles of one env): lane l
-// holds pixel l of every one of them. Per step a lane issues the gathers of all its live rays before
-// using any, so RPL independent loads per lane are in flight at once — the
-// march is bound by gather latency, and this multiplies the loads in flight
-// without more waves. Lanes of dead rays point their load past the end of
-// the buffer range, where the hardware returns 0 without a cache access.
+// holds pixel l of every one of them. Per step a lane issues the gathers of
+// all its live rays before using any, so RPL independent loads per lane are
+// in flight at once. The loop is bound by the texture path (L1 tag lookups
+// of divergent gathers) and by vector instruction issue, about equally.
 //
 // The step counter is wave-uniform and the loop leaves as soon as no ray of
 // the wave is alive, which is exact: alive only turns off and a dead ray adds
@@ -621,9 +620,9 @@ __global__ __launch_bounds__(64 * kTileWaves) void march_tiles(MarchArgs a) {
     const uint32_t* __restrict__ tab = s_axis;
     // Liveness is kept as one 64-bit lane mask per tile (scalar registers):
     // a new mask is the old one ANDed with the ballots of the two compares,
-    // and inverse_ballot turns it back into the per-lane predicate, so no
-    // vector instruction is spent on bookkeeping. A tile whose rays have all
-    // ended skips its address math and gather.
+    // and inverse_ballot turns it back into the per-lane predicate (the exec
+    // mask of the address math and gather), so no vector instruction is spent
+    // on bookkeeping. A tile whose rays have all ended skips both.
     uint64_t live[RPL];
 #pragma unroll
     for (int j = 0; j < RPL; ++j) live[j] = __builtin_amdgcn_ballot_w64(alive[j]);
@@ -636,16 +635,14 @@ __global__ __launch_bounds__(64 * kTileWaves) void march_tiles(MarchArgs a) {
 #pragma unroll
         for (int j = 0; j < RPL; ++j) {
             float s = 0.0f;
-            if (live[j] != 0) {
-                const bool l = __builtin_amdgcn_inverse_ballot_w64(live[j]);
+            if (__builtin_amdgcn_inverse_ballot_w64(live[j])) {   // ended lanes issue no gather
                 const float px = ex[j] + dx[j] * t[j];
                 const float py = ey[j] + dy[j] * t[j];
                 const float pz = ez[j] + dz[j] * t[j];
                 const int ix = (int)__builtin_amdgcn_fmed3f((px - a.mnx) * a.inv_cell, 0.0f, a.fnx1);
                 const int iy = (int)__builtin_amdgcn_fmed3f((py - a.mny) * a.inv_cell, 0.0f, a.fny1);
                 const int iz = (int)__builtin_amdgcn_fmed3f((pz - a.mnz) * a.inv_cell, 0.0f, a.fnz1);
-                const uint32_t off = l ? tab[ix] + tab[a.nx + iy] + tab[a.nx + a.ny + iz] : a.dead_off;
-                s = load_voxel<GT>(rsrc, off);
+                s = load_voxel<GT>(rsrc, tab[ix] + tab[a.nx + iy] + tab[a.nx + a.ny + iz]);
             }
             sd[j] = s;
         }
