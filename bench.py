@@ -68,6 +68,49 @@ def cpu_baseline(w, sc, envs, repeats=3):
                       f"median of {repeats}: {t * 1e3:.1f} ms; cpu: {model}"}
 
 
+class HipEvents:
+    """Timing events made up front with the HIP runtime torch has loaded
+    (hipEventCreate), each recorded once in the timed loop. torch's events
+    are created lazily at their first record, inside the loop, and that
+    occasionally stalled the host for ~25 ms mid-run; re-recording events
+    created beforehand slowed some renders instead."""
+
+    def __init__(self, n):
+        import ctypes
+        self._c = ctypes
+        lib = ctypes.CDLL("libamdhip64.so.7")       # the instance torch already loaded
+        vp = ctypes.c_void_p
+        lib.hipEventCreate.argtypes = [ctypes.POINTER(vp)]
+        lib.hipEventRecord.argtypes = [vp, vp]
+        lib.hipEventElapsedTime.argtypes = [ctypes.POINTER(ctypes.c_float), vp, vp]
+        lib.hipEventDestroy.argtypes = [vp]
+        self._lib = lib
+        self.ev = []
+        for _ in range(n):
+            h = vp()
+            self._check(lib.hipEventCreate(ctypes.byref(h)), "hipEventCreate")
+            self.ev.append(h)
+
+    @staticmethod
+    def _check(rc, what):
+        if rc != 0:
+            raise RuntimeError(f"{what} failed ({rc})")
+
+    def record(self, i, stream):
+        self._check(self._lib.hipEventRecord(self.ev[i], stream), "hipEventRecord")
+
+    def ms(self, i, j):
+        out = self._c.c_float()
+        self._check(self._lib.hipEventElapsedTime(self._c.byref(out), self.ev[i], self.ev[j]),
+                    "hipEventElapsedTime")
+        return out.value
+
+    def close(self):
+        for h in self.ev:
+            self._lib.hipEventDestroy(h)
+        self.ev = []
+
+
 def profiled_traffic(key):
     """L2-miss traffic per launch recorded for this configuration by the
     FETCH_SIZE / WRITE_SIZE counter runs summarised under profiles/ (a line
@@ -365,24 +408,22 @@ def main(argv=None):
     stream = torch.cuda.current_stream(dev)
     for _ in range(args.warmup):
         step()
+    # events 0 and 1 bracket the timed region, 2 + 2k and 3 + 2k step k
+    ev = HipEvents(2 + 2 * args.steps)
+    sp = stream.cuda_stream
     torch.cuda.synchronize()
-    ev0 = torch.cuda.Event(enable_timing=True)
-    ev1 = torch.cuda.Event(enable_timing=True)
-    per = []
     t_start = time.perf_counter()
-    ev0.record(stream)
-    for _ in range(args.steps):
-        e_a = torch.cuda.Event(enable_timing=True)
-        e_b = torch.cuda.Event(enable_timing=True)
-        e_a.record(stream)
+    ev.record(0, sp)
+    for k in range(args.steps):
+        ev.record(2 + 2 * k, sp)
         step()
-        e_b.record(stream)
-        per.append((e_a, e_b))
-    ev1.record(stream)
+        ev.record(3 + 2 * k, sp)
+    ev.record(1, sp)
     torch.cuda.synchronize()
     wall = time.perf_counter() - t_start
-    total_ms = ev0.elapsed_time(ev1)
-    launch_ms = [a.elapsed_time(b) for a, b in per]
+    total_ms = ev.ms(0, 1)
+    launch_ms = [ev.ms(2 + 2 * k, 3 + 2 * k) for k in range(args.steps)]
+    ev.close()
     ms_per_step = total_ms / args.steps
     avg_launch_ms = sum(launch_ms) / len(launch_ms)
     med_launch_ms = statistics.median(launch_ms)
