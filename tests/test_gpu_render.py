@@ -47,11 +47,11 @@ def _depth(enc, near, rng):
 
 
 def _lidar(dev, w, sc, **kw):
-    args = dict(range_units=w.range_units, near_range=w.near_range, max_steps=w.max_steps,
-                hit_eps=w.hit_eps, grid_dtype=torch.float32, device=dev)
+    args = dict(width=w.width, height=w.height, range_units=w.range_units,
+                near_range=w.near_range, max_steps=w.max_steps, hit_eps=w.hit_eps,
+                grid_dtype=torch.float32, device=dev)
     args.update(kw)
-    return vision.GpuLidar.from_grid(sc.sdf, sc.mins, sc.cell, width=w.width, height=w.height,
-                                     **args)
+    return vision.GpuLidar.from_grid(sc.sdf, sc.mins, sc.cell, **args)
 
 
 def _gpu_render(lid, ps, dev, **kw):
@@ -116,6 +116,31 @@ def test_f16_store_matches_the_oracle_on_the_rounded_grid(dev):
     got = _gpu_render(lid, ps, dev).cpu().numpy()
     want, _ = _oracle(w, sc, ps, store="f16")
     _assert_parity(got, want, w, "ramp_field/f16")
+
+
+@pytest.mark.parametrize("name,n,size", [("ramp_field", 96, None), ("small_ramps", 16, None),
+                                         ("ramp_field", 23, (37, 19)), ("small_ramps", 9, (8, 8))])
+def test_f16_slot_packing_is_exact(dev, name, n, size):
+    """fp16 grids march with slot packing (a wave's two tiles merged into one
+    slot once their live rays fit 64 lanes): images and per-ray load counts
+    equal the oracle's on the f16-rounded grid bit for bit, in both tile
+    orders. 37x19 images give waves whose two tiles lie in different envs
+    (no packing there) and lanes without a pixel; 8x8 images give one tile
+    per env."""
+    w, sc = _scene(name)
+    ps = w.poses(sc, n)
+    W, H = size if size else (w.width, w.height)
+    _say(f"case f16 packing {name} n={n} {W}x{H}")
+    lid = _lidar(dev, w, sc, grid_dtype=torch.float16, width=W, height=H)
+    assert lid.rays_per_lane == 2
+    want, want_taps = _oracle(w, sc, ps, store="f16", width=W, height=H)
+    for order in ("lookahead", "launch"):
+        lid.set_tile_order(order, min_tiles=0)
+        taps = torch.full((n, H, W), -1, dtype=torch.int32, device=dev)
+        got = torch.full((n, H, W), -1.0, device=dev)
+        _gpu_render(lid, ps, dev, out=got, taps=taps)
+        assert np.array_equal(got.cpu().numpy(), want), order
+        assert np.array_equal(taps.cpu().numpy(), want_taps), order
 
 
 def test_bf16_output_is_the_rounded_f32_output(dev):
