@@ -34,7 +34,7 @@ extern "C" {
 
 /* Bumped on every struct or semantic change; the binding refuses a library
  * reporting another value. */
-#define SDFR_ABI_VERSION 7
+#define SDFR_ABI_VERSION 8
 
 /* Element types of caller arrays. */
 enum {
@@ -183,8 +183,9 @@ SDFR_API int64_t sdfr_grid_bytes(const SdfrGrid* grid);
 
 /* Device bytes of the workspace sdfr_render needs for n_envs envs of this
  * camera: per env (W + H + 4) float2 of ray tables, then for the tile order
- * one int32 and one uint16 per 8x8 tile and 2 x 4096 uint32 buckets (each
- * part 256-byte aligned). < 0 on bad arguments. */
+ * one int32, one uint16 and one uint32 per 8x8 tile (each part 256-byte
+ * aligned). < 0 on bad arguments. The tile order's bucket counts live in
+ * the grid handle. */
 SDFR_API int64_t sdfr_workspace_bytes(const SdfrCam* cam, int32_t n_envs);
 
 /* Renders N depth images: equiangular (or pinhole) rays from each env's eye,

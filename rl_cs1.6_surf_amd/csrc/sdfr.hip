@@ -23,13 +23,14 @@
 // are evaluated in fp64 and rounded once to fp32, which gives the correctly
 // rounded fp32 value except in cases rarer than 1 in 2^28.
 //
-// One render is two to four launches on the caller's stream:
-//   1. ray_tables: per env, the (sin, cos) of its H row pitch angles and W
+// One render is two or three launches on the caller's stream:
+//   1. ray_setup: per env, the (sin, cos) of its H row pitch angles and W
 //      column yaw angles, and its eye point — all the transcendental work of
 //      ray setup, (H+W) fp64 sincos per env instead of two per ray;
-//   2. (tiles schedule, lookahead order) order_count + order_scatter: a
-//      counting sort of the tiles by where they look (see "tile order");
-//   3. the march, in one of three schedules with identical results:
+//      With the lookahead tile order the same launch also keys the tiles by
+//      where they look and counts them into buckets, and order_scatter
+//      writes the sorted list (see "tile order");
+//   2. the march, in one of three schedules with identical results:
 //      - tiles (default): launch-scheduled two-wave workgroups, each wave
 //        marching 8x8 pixel tiles with RPL rays per lane in flight at once;
 //      - persistent: a grid that fills the GPU once; each wave keeps 64 ray
@@ -122,6 +123,7 @@ struct SdfrGrid {
     int cus;               // compute units of the device
     int32_t tile_order;    // SDFR_ORDER_*: the order the tiles schedule takes tiles in
     int64_t order_min_tiles;  // ... applied to renders of at least this many tiles
+    uint32_t* order_hist;  // tile-order bucket counts [kOrderBuckets]: zero between renders
 };
 
 namespace {
@@ -250,9 +252,10 @@ struct MarchArgs {
     const void* nzmask;           // surf mask: |n_z|*127 int8 copy, same layout
     uint32_t nz_bytes;
     int32_t* perm;                // tiles schedule: logical unit -> unit, or null
-    uint32_t* order_hist;         // tile-order bucket counts [kOrderBuckets], then cursors
-                                  // [kOrderBuckets] (zeroed by the ray-table kernel), or null
+    uint32_t* order_hist;         // tile-order bucket counts [kOrderBuckets] (the handle's:
+                                  // zero on entry, zeroed again by the march), or null
     uint16_t* order_key;          // bucket of each sorted unit
+    uint32_t* order_rank;         // place of each unit within its bucket
     int order_shift;              // voxel index >> shift = tile-order cell
     float lookahead;              // distance along a unit's centre ray that keys it
     int order_unit;               // tiles per sorted unit: one workgroup's, kTileWaves * RPL
@@ -302,6 +305,12 @@ __device__ __forceinline__ float eye_sample(const MarchArgs& a, float ex, float 
     return a.grid_f16 ? load_voxel<__half>(rsrc, off) : load_voxel<float>(rsrc, off);
 }
 
+// Eye height of env n: origin z + 12 ducked or 17 standing (vision.py:77-78).
+__device__ __forceinline__ float eye_z(const MarchArgs& a, int n) {
+    const bool dk = read_ducked(a.ducked, n * a.ducked_stride, a.ducked_dtype);
+    return a.origin[n * a.origin_stride + 2] + (dk ? 12.0f : 17.0f);
+}
+
 // Ray table of env n, entries (float2):
 //   [0, H)       rows:    equiangular (sin, cos) of pitch + poff[r];  pinhole (v[r], 0)
 //   [H, H+W)     columns: equiangular (sin, cos) of yaw + yoff[c];    pinhole (u[c], 0)
@@ -324,8 +333,7 @@ __device__ __forceinline__ float2 table_entry(const MarchArgs& a, int n, int e) 
     e -= a.W;
     if (e == 0) return make_float2(a.origin[n * a.origin_stride + 0], a.origin[n * a.origin_stride + 1]);
     if (e == 1) {
-        const bool dk = read_ducked(a.ducked, n * a.ducked_stride, a.ducked_dtype);
-        const float ez = a.origin[n * a.origin_stride + 2] + (dk ? 12.0f : 17.0f);
+        const float ez = eye_z(a, n);
         return make_float2(ez, eye_sample(a, a.origin[n * a.origin_stride + 0],
                                           a.origin[n * a.origin_stride + 1], ez));
     }
@@ -396,19 +404,6 @@ __device__ __forceinline__ void fill_axis_tables(const MarchArgs& a, uint32_t* s
     __syncthreads();
 }
 
-// ------------------------------------------------------------ ray tables --
-__global__ __launch_bounds__(256) void ray_tables_kernel(MarchArgs a) {
-    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    // the tile order's buckets start from zero (a kernel, not a memset, so
-    // a captured render replays correctly)
-    if (a.order_hist)
-        for (int64_t b = i; b < 2 * kOrderBuckets; b += (int64_t)gridDim.x * blockDim.x) a.order_hist[b] = 0u;
-    if (i >= (int64_t)a.n_envs * a.rt_stride) return;
-    const int n = (int)(i / a.rt_stride);
-    const int e = (int)(i - (int64_t)n * a.rt_stride);
-    a.rt[i] = table_entry(a, n, e);
-}
-
 // ------------------------------------------------------------- tile order --
 // The tiles schedule can take tiles in a spatial order instead of env order.
 // Tiles are sorted in units of one workgroup's tiles (kTileWaves * RPL
@@ -421,13 +416,23 @@ __global__ __launch_bounds__(256) void ray_tables_kernel(MarchArgs a) {
 // sorted list to the XCDs (xcd_chunked_block), so at any time each XCD's L2
 // serves rays that look at one part of the map. Results do not depend on the
 // order (every tile is marched exactly as before); it only changes which
-// rays share a cache. Two small kernels, count and scatter, after the
-// ray-table kernel has zeroed the buckets.
+// rays share a cache.
+//
+// The sort is two passes. The ray-setup launch keys the units, counts them
+// per bucket in LDS and adds each block's counts to the handle's bucket
+// counts with one atomic per bucket, whose return value places the block's
+// units of that bucket after those of the blocks before it (each unit's
+// rank within its bucket). order_scatter scans the counts and writes each
+// unit to its bucket's start plus its rank. The march zeroes the counts
+// again, so the next render (or graph replay) starts from zero.
 __device__ __forceinline__ uint32_t spread_bits4(uint32_t v) {
     v &= 15u;
     return (v & 1u) | ((v & 2u) << 2) | ((v & 4u) << 4) | ((v & 8u) << 6);
 }
 
+// The key of a unit, from its centre ray, in fast fp32 arithmetic (the ray
+// tables are written by the same launch); the key only orders the tiles, so
+// its precision does not touch the results.
 template <int CAMERA>
 __device__ __forceinline__ uint32_t tile_order_key(const MarchArgs& a, int64_t unit) {
     // the unit's centre pixel: the left edge of its middle tile, or the
@@ -440,63 +445,93 @@ __device__ __forceinline__ uint32_t tile_order_key(const MarchArgs& a, int64_t u
     const int ty = rem / a.tiles_x;
     const int tx = rem - ty * a.tiles_x;
     const int r = min(ty * 8 + 4, a.H - 1), c = min(tx * 8 + (whole ? 0 : 4), a.W - 1);
-    const float2* rt = a.rt + (int64_t)n * a.rt_stride;
-    const float2 e01 = rt[a.H + a.W], e2 = rt[a.H + a.W + 1];
-    float2 psc = make_float2(0.f, 0.f), ysc = make_float2(0.f, 0.f);
+    const float yr = a.yaw[n * a.yaw_stride] * kD2Rf;
+    const float pr = a.pitch[n * a.pitch_stride] * kD2Rf;
+    float2 row, col, psc = make_float2(0.f, 0.f), ysc = make_float2(0.f, 0.f);
     if constexpr (CAMERA == SDFR_CAM_PINHOLE) {
-        psc = rt[a.H + a.W + 2];
-        ysc = rt[a.H + a.W + 3];
+        row = make_float2(pinhole_v(r, a.H, a.tan_v), 0.0f);
+        col = make_float2(pinhole_u(c, a.W, a.tan_h), 0.0f);
+        psc = make_float2(__sinf(pr), __cosf(pr));
+        ysc = make_float2(__sinf(yr), __cosf(yr));
+    } else {
+        const float p = pr + (float)a.vfov * (0.5f - ((float)r + 0.5f) / (float)a.H) * kD2Rf;
+        const float y = yr + (float)a.hfov * (0.5f - ((float)c + 0.5f) / (float)a.W) * kD2Rf;
+        row = make_float2(__sinf(p), __cosf(p));
+        col = make_float2(__sinf(y), __cosf(y));
     }
-    const float3 d = ray_dir<CAMERA>(rt[r], rt[a.H + c], psc, ysc);
+    const float3 d = ray_dir<CAMERA>(row, col, psc, ysc);
     const float L = a.lookahead;
-    const int ix = (int)__builtin_amdgcn_fmed3f((e01.x + d.x * L - a.mnx) * a.inv_cell, 0.0f, a.fnx1);
-    const int iy = (int)__builtin_amdgcn_fmed3f((e01.y + d.y * L - a.mny) * a.inv_cell, 0.0f, a.fny1);
-    const int iz = (int)__builtin_amdgcn_fmed3f((e2.x + d.z * L - a.mnz) * a.inv_cell, 0.0f, a.fnz1);
+    const float ex = a.origin[n * a.origin_stride + 0], ey = a.origin[n * a.origin_stride + 1];
+    const float ez = eye_z(a, n);
+    const int ix = (int)__builtin_amdgcn_fmed3f((ex + d.x * L - a.mnx) * a.inv_cell, 0.0f, a.fnx1);
+    const int iy = (int)__builtin_amdgcn_fmed3f((ey + d.y * L - a.mny) * a.inv_cell, 0.0f, a.fny1);
+    const int iz = (int)__builtin_amdgcn_fmed3f((ez + d.z * L - a.mnz) * a.inv_cell, 0.0f, a.fnz1);
     return spread_bits4((uint32_t)ix >> a.order_shift) |
            (spread_bits4((uint32_t)iy >> a.order_shift) << 1) |
            (spread_bits4((uint32_t)iz >> a.order_shift) << 2);
 }
 
-// Both passes give each block the same chunk of kOrderChunk units; buckets
-// are counted (and ranked) in LDS, so a block touches each global bucket
-// at most once per pass.
+// Units per sort block (4 per thread).
 constexpr int kOrderChunk = 1024;
 
+// ------------------------------------------------------------- ray setup --
+// Blocks [0, table_blocks) fill the ray tables, one entry per thread; with
+// the tile order on, blocks from table_blocks on key and count a chunk of
+// kOrderChunk units each.
 template <int CAMERA>
-__global__ __launch_bounds__(256) void order_count(MarchArgs a) {
+__global__ __launch_bounds__(256) void ray_setup(MarchArgs a, int table_blocks) {
+    if ((int)blockIdx.x < table_blocks) {
+        const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+        if (i >= (int64_t)a.n_envs * a.rt_stride) return;
+        const int n = (int)(i / a.rt_stride);
+        const int e = (int)(i - (int64_t)n * a.rt_stride);
+        a.rt[i] = table_entry(a, n, e);
+        return;
+    }
+    constexpr int kPer = kOrderChunk / 256;
     __shared__ uint32_t h[kOrderBuckets];
     for (int i = threadIdx.x; i < kOrderBuckets; i += blockDim.x) h[i] = 0u;
     __syncthreads();
-    const int64_t t0 = (int64_t)blockIdx.x * kOrderChunk;
-    for (int k = threadIdx.x; k < kOrderChunk; k += blockDim.x) {
-        const int64_t t = t0 + k;
-        if (t < a.order_units) {
-            const uint32_t key = tile_order_key<CAMERA>(a, t);
-            a.order_key[t] = (uint16_t)key;
-            atomicAdd(&h[key], 1u);
+    const int64_t u0 = (int64_t)(blockIdx.x - table_blocks) * kOrderChunk;
+    uint32_t key[kPer], rank[kPer];
+#pragma unroll
+    for (int j = 0; j < kPer; ++j) {
+        const int64_t u = u0 + threadIdx.x + j * 256;
+        key[j] = 0u;
+        rank[j] = 0u;
+        if (u < a.order_units) {
+            key[j] = tile_order_key<CAMERA>(a, u);
+            rank[j] = atomicAdd(&h[key[j]], 1u);
         }
     }
     __syncthreads();
-    for (int i = threadIdx.x; i < kOrderBuckets; i += blockDim.x)
-        if (h[i]) atomicAdd(&a.order_hist[i], h[i]);
+    // this block's first place in each bucket
+    for (int b = threadIdx.x; b < kOrderBuckets; b += blockDim.x)
+        if (h[b]) h[b] = atomicAdd(&a.order_hist[b], h[b]);
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < kPer; ++j) {
+        const int64_t u = u0 + threadIdx.x + j * 256;
+        if (u < a.order_units) {
+            a.order_key[u] = (uint16_t)key[j];
+            a.order_rank[u] = h[key[j]] + rank[j];
+        }
+    }
 }
 
 // Each block scans the 4096 bucket counts in LDS (bucket b's first slot in
-// the sorted list), reserves a run of slots per bucket for its chunk's units
-// from the bucket cursors, and writes each unit into its slot.
+// the sorted list) and writes its chunk's units to their slots.
 __global__ __launch_bounds__(256) void order_scatter(MarchArgs a) {
     constexpr int kPer = kOrderChunk / 256;
     constexpr int kBinsPer = kOrderBuckets / 256;
     __shared__ uint32_t start[kOrderBuckets];  // bucket b's first slot
-    __shared__ uint32_t cnt[kOrderBuckets];    // this chunk's tiles per bucket
     __shared__ uint32_t wave_sum[4];
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-    // exclusive scan of the global counts: 16 buckets per thread
+    // exclusive scan of the counts: 16 buckets per thread
     uint32_t v[kBinsPer], sum = 0;
     for (int j = 0; j < kBinsPer; ++j) {
         v[j] = a.order_hist[tid * kBinsPer + j];
         sum += v[j];
-        cnt[tid * kBinsPer + j] = 0u;
     }
     uint32_t inc = sum;
     for (int off = 1; off < 64; off <<= 1) {
@@ -512,24 +547,12 @@ __global__ __launch_bounds__(256) void order_scatter(MarchArgs a) {
         run += v[j];
     }
     __syncthreads();
-    // rank this chunk's units within their buckets
-    const int64_t t0 = (int64_t)blockIdx.x * kOrderChunk;
-    uint32_t key[kPer], rank[kPer];
+    const int64_t u0 = (int64_t)blockIdx.x * kOrderChunk;
     for (int j = 0; j < kPer; ++j) {
-        const int64_t t = t0 + tid + j * 256;
-        key[j] = t < a.order_units ? a.order_key[t] : 0u;
-        rank[j] = t < a.order_units ? atomicAdd(&cnt[key[j]], 1u) : 0u;
-    }
-    __syncthreads();
-    uint32_t* cursor = a.order_hist + kOrderBuckets;
-    for (int i = tid; i < kOrderBuckets; i += blockDim.x)
-        if (cnt[i]) start[i] += atomicAdd(&cursor[i], cnt[i]);
-    __syncthreads();
-    for (int j = 0; j < kPer; ++j) {
-        const int64_t t = t0 + tid + j * 256;
-        if (t >= a.order_units) continue;
-        const uint32_t pos = start[key[j]] + rank[j];
-        if ((int64_t)pos < a.order_units) a.perm[pos] = (int32_t)t;
+        const int64_t u = u0 + tid + j * 256;
+        if (u >= a.order_units) continue;
+        const uint32_t pos = start[a.order_key[u] & (kOrderBuckets - 1)] + a.order_rank[u];
+        if ((int64_t)pos < a.order_units) a.perm[pos] = (int32_t)u;
     }
 }
 
@@ -574,6 +597,9 @@ __global__ __launch_bounds__(64 * kTileWaves) void march_tiles(MarchArgs a) {
     fill_axis_tables<GT, LAYOUT>(a, s_axis);
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int lane = threadIdx.x & 63;
+    if (a.order_hist)   // the sort's counts are spent: clear them for the next render
+        for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < kOrderBuckets; i += gridDim.x * blockDim.x)
+            a.order_hist[i] = 0u;
     const int blk = a.perm ? xcd_chunked_block(blockIdx.x, a.nblocks, kXcdChunk)
                            : xcd_logical_block(blockIdx.x, a.nblocks);
     const int64_t tile0 = ((int64_t)blk * kTileWaves + wave) * RPL;
@@ -1150,27 +1176,17 @@ void launch_slots(MarchArgs& a, const SdfrGrid* g, size_t lds, hipStream_t st) {
     }
 }
 
-template <int CAMERA>
-void launch_tile_order(const MarchArgs& a, hipStream_t st) {
-    if (!a.perm) return;
-    const int chunks = (int)((a.order_units + kOrderChunk - 1) / kOrderChunk);
-    order_count<CAMERA><<<chunks, 256, 0, st>>>(a);
-    order_scatter<<<chunks, 256, 0, st>>>(a);
-}
-
 template <typename GT, int LAYOUT, int OUT, int CAMERA, bool CENSUS>
 void launch_march(MarchArgs& a, const SdfrGrid* g, bool surf, hipStream_t st) {
     if (surf) {
         // the surf-mask variant exists for the equiangular camera only
         // (vision.py:463-467) and always runs the tiles schedule
         if constexpr (CAMERA == SDFR_CAM_EQUIANGULAR) {
-            launch_tile_order<CAMERA>(a, st);
             launch_tiles<GT, LAYOUT, OUT, CAMERA, CENSUS, true>(a, g->rays_per_lane, st);
         }
         return;
     }
     if (g->schedule == SDFR_SCHED_TILES) {
-        launch_tile_order<CAMERA>(a, st);
         launch_tiles<GT, LAYOUT, OUT, CAMERA, CENSUS, false>(a, g->rays_per_lane, st);
         return;
     }
@@ -1271,8 +1287,8 @@ void fill_args(MarchArgs* a, const SdfrCam* cam, const SdfrPoses* poses) {
     a->rt_stride = cam->width + cam->height + 4;
 }
 
-// Render workspace: the ray tables, then the tile order's permutation and
-// buckets, each 256-byte aligned.
+// Render workspace: the ray tables, then the tile order's permutation, keys
+// and ranks (one per unit, sized for one per tile), each 256-byte aligned.
 int64_t align256(int64_t v) { return (v + 255) & ~(int64_t)255; }
 
 int64_t ray_table_bytes(int width, int height, int n_envs) {
@@ -1282,8 +1298,7 @@ int64_t ray_table_bytes(int width, int height, int n_envs) {
 int64_t workspace_bytes(int width, int height, int n_envs) {
     const int64_t tiles = (int64_t)((width + 7) / 8) * ((height + 7) / 8) * n_envs;
     return ray_table_bytes(width, height, n_envs) + align256(tiles * (int64_t)sizeof(int32_t)) +
-           align256(tiles * (int64_t)sizeof(uint16_t)) +
-           2 * (int64_t)kOrderBuckets * (int64_t)sizeof(uint32_t);
+           align256(tiles * (int64_t)sizeof(uint16_t)) + align256(tiles * (int64_t)sizeof(uint32_t));
 }
 
 }  // namespace
@@ -1381,6 +1396,7 @@ SDFR_API SdfrGrid* sdfr_grid_create(const SdfrGridDesc* desc, const void* src, i
     g->cus = 0;
     g->tile_order = SDFR_ORDER_LOOKAHEAD;
     g->order_min_tiles = kOrderMinTiles;
+    g->order_hist = nullptr;
     hipError_t e = hipGetDevice(&g->device);
     if (e == hipSuccess)
         e = hipDeviceGetAttribute(&g->cus, hipDeviceAttributeMultiprocessorCount, g->device);
@@ -1391,6 +1407,8 @@ SDFR_API SdfrGrid* sdfr_grid_create(const SdfrGridDesc* desc, const void* src, i
     if (e == hipSuccess) e = hipMalloc(&g->data, (size_t)g->bytes);
     if (e == hipSuccess) e = hipMalloc((void**)&g->counters, sizeof(uint32_t) * kCounterWords);
     if (e == hipSuccess) e = hipMemsetAsync(g->counters, 0, sizeof(uint32_t) * kCounterWords, st);
+    if (e == hipSuccess) e = hipMalloc((void**)&g->order_hist, sizeof(uint32_t) * kOrderBuckets);
+    if (e == hipSuccess) e = hipMemsetAsync(g->order_hist, 0, sizeof(uint32_t) * kOrderBuckets, st);
     if (e == hipSuccess && !src_on_device) {
         e = hipMalloc(&staged, (size_t)src_bytes);
         if (e == hipSuccess)
@@ -1414,6 +1432,7 @@ SDFR_API SdfrGrid* sdfr_grid_create(const SdfrGridDesc* desc, const void* src, i
         copy_err(err, errlen);
         if (g->data) (void)hipFree(g->data);
         if (g->counters) (void)hipFree(g->counters);
+        if (g->order_hist) (void)hipFree(g->order_hist);
         delete g;
         return nullptr;
     }
@@ -1425,6 +1444,7 @@ SDFR_API void sdfr_grid_destroy(SdfrGrid* grid) {
     if (grid->data) (void)hipFree(grid->data);
     if (grid->nz_data) (void)hipFree(grid->nz_data);
     if (grid->counters) (void)hipFree(grid->counters);
+    if (grid->order_hist) (void)hipFree(grid->order_hist);
     delete grid;
 }
 
@@ -1556,6 +1576,7 @@ SDFR_API int32_t sdfr_render(const SdfrGrid* grid, const SdfrCam* cam, const Sdf
     a.perm = nullptr;
     a.order_hist = nullptr;
     a.order_key = nullptr;
+    a.order_rank = nullptr;
     a.order_shift = 0;
     a.lookahead = kOrderLookahead * cam->near;
     a.order_unit = kTileWaves * grid->rays_per_lane;
@@ -1569,14 +1590,21 @@ SDFR_API int32_t sdfr_render(const SdfrGrid* grid, const SdfrCam* cam, const Sdf
         a.order_key = (uint16_t*)ws;
         a.logical_tiles = a.order_units * a.order_unit;
         ws += align256(a.total_tiles * (int64_t)sizeof(uint16_t));
-        a.order_hist = (uint32_t*)ws;
+        a.order_rank = (uint32_t*)ws;
+        a.order_hist = grid->order_hist;
         const int maxdim = max(a.nx, max(a.ny, a.nz));
         while (((maxdim - 1) >> a.order_shift) >= (1 << kOrderCellsLog)) ++a.order_shift;
     }
 
     hipStream_t st = (hipStream_t)stream;
     const int64_t entries = (int64_t)poses->n_envs * a.rt_stride;
-    ray_tables_kernel<<<(int)((entries + 255) / 256), 256, 0, st>>>(a);
+    const int table_blocks = (int)((entries + 255) / 256);
+    const int sort_blocks = a.perm ? (int)((a.order_units + kOrderChunk - 1) / kOrderChunk) : 0;
+    if (cam->camera == SDFR_CAM_PINHOLE)
+        ray_setup<SDFR_CAM_PINHOLE><<<table_blocks + sort_blocks, 256, 0, st>>>(a, table_blocks);
+    else
+        ray_setup<SDFR_CAM_EQUIANGULAR><<<table_blocks + sort_blocks, 256, 0, st>>>(a, table_blocks);
+    if (sort_blocks) order_scatter<<<sort_blocks, 256, 0, st>>>(a);
     const bool census = image->taps != nullptr;
     if (grid->store_dtype == SDFR_F16) {
         if (grid->layout == SDFR_LAYOUT_BRICK4)

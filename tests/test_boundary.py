@@ -113,11 +113,11 @@ def test_render_rejects_bad_arguments_without_a_device():
     rc = lib.sdfr_render(None, ctypes.byref(_cam()), ctypes.byref(_poses()), ctypes.byref(img),
                          None, 0, None)
     assert rc == -1 and "grid" in _sdfr.last_error()
-    # ray tables, an int32 and a uint16 per 8x8 tile, 2 x 4096 buckets (parts 256-byte aligned)
+    # ray tables, then an int32, a uint16 and a uint32 per 8x8 tile (parts 256-byte aligned)
     assert lib.sdfr_workspace_bytes(ctypes.byref(_cam()), 2048) == (
-        2048 * (128 + 64 + 4) * 8 + 2048 * 128 * 4 + 2048 * 128 * 2 + 2 * 4096 * 4)
+        2048 * (128 + 64 + 4) * 8 + 2048 * 128 * 4 + 2048 * 128 * 2 + 2048 * 128 * 4)
     c = _cam(width=9, height=5)
-    assert lib.sdfr_workspace_bytes(ctypes.byref(c), 3) == 512 + 256 + 256 + 2 * 4096 * 4
+    assert lib.sdfr_workspace_bytes(ctypes.byref(c), 3) == 512 + 256 + 256 + 256
     assert lib.sdfr_workspace_bytes(ctypes.byref(_cam()), 0) < 0
     # the grid check comes first; the argument checks are shared with sdfr_ray_dirs
     cases = [
