@@ -262,6 +262,40 @@ def test_closed_form_constant_field(dev):
         assert np.all(out == np.float32(want_t) / np.float32(rng)), (max_steps, out.ravel()[:3])
 
 
+@pytest.mark.parametrize("max_steps,hit_eps,rng", [
+    (0, 1.0, 1536.0), (1, 1.0, 1536.0), (2, 1.0, 1536.0), (3, -1.0, 1536.0),
+    (64, 0.0, 1536.0), (64, 1.0, 0.0), (64, 1.0, -5.0), (64, -1.0, 300.0)])
+def test_step_rule_corners_are_exact_in_every_schedule(dev, max_steps, hit_eps, rng):
+    """The step rule at its edges (vision.py:100-112): no steps, the first
+    step only (taken from the eye sample), a hit_eps that nothing reaches or
+    that 0 distance does not pass, a range that ends every ray at t = 0 or
+    that the march overshoots. Images and per-ray load counts equal the
+    oracle's bit for bit in every schedule, both tile orders and on f16
+    grids (slot packing)."""
+    w, sc = _scene("small_ramps")
+    n = 6
+    ps = w.poses(sc, n)
+    _say(f"case step corners max_steps={max_steps} hit_eps={hit_eps} range={rng}")
+    kw = dict(range_units=rng, near_range=1000.0, max_steps=max_steps, hit_eps=hit_eps)
+    for store, gdt in (("f32", torch.float32), ("f16", torch.float16)):
+        want, want_taps = oracle.render(sc.sdf, sc.mins, sc.cell, ps.origin, ps.yaw, ps.pitch,
+                                        ps.ducked, width=w.width, height=w.height, store=store,
+                                        threads=8, **kw)
+        lid = vision.GpuLidar.from_grid(sc.sdf, sc.mins, sc.cell, width=w.width,
+                                        height=w.height, grid_dtype=gdt, device=dev, **kw)
+        for sched, rpl, order in (("tiles", 2, "lookahead"), ("tiles", 2, "launch"),
+                                  ("tiles", 1, "lookahead"), ("slots", 2, "launch"),
+                                  ("persistent", None, "launch")):
+            lid.set_schedule(sched, rays_per_lane=rpl)
+            lid.set_tile_order(order, min_tiles=0)
+            taps = torch.full((n, w.height, w.width), -1, dtype=torch.int32, device=dev)
+            got = torch.full((n, w.height, w.width), -1.0, device=dev)
+            _gpu_render(lid, ps, dev, out=got, taps=taps)
+            label = (store, sched, rpl, order)
+            assert np.array_equal(got.cpu().numpy(), want), label
+            assert np.array_equal(taps.cpu().numpy(), want_taps), label
+
+
 @pytest.mark.parametrize("W,H,n", [(9, 5, 3), (33, 33, 2), (1, 1, 5), (20, 12, 7)])
 def test_ragged_images_match_the_oracle(dev, W, H, n):
     """Image sizes that do not fill whole 8x8 tiles, and tiny N."""
