@@ -71,6 +71,13 @@ constexpr int kCtrStride = 32;
 constexpr int kCounterWords = (kParts + 1) * kCtrStride;
 // Grids up to this size stay resident in the 256 MB Infinity Cache.
 constexpr int64_t kCacheResidentBytes = 192ll << 20;
+// On larger grids the march is bound by L2-miss traffic, and fewer rays in
+// flight per XCD raise the L2 hit rate more than they cost in latency: the
+// tiles schedule then holds at most this many workgroups per CU (by sizing
+// their LDS), 24 waves instead of 32. Measured on a 1 GiB grid: 12 per CU
+// 2.09 ms, 10 2.10, 16 (unlimited) 2.15, 5 2.55; on a cache-resident grid any
+// cap is slower.
+constexpr int kSpillBlocksPerCU = 12;
 // Tile order: 16 cells per axis at most, Morton-numbered buckets.
 constexpr int kOrderCellsLog = 4;
 constexpr int kOrderBuckets = 1 << (3 * kOrderCellsLog);
@@ -121,6 +128,7 @@ struct SdfrGrid {
     int64_t nz_bytes;
     int device;
     int cus;               // compute units of the device
+    int lds_per_cu;        // bytes of LDS per CU
     int32_t tile_order;    // SDFR_ORDER_*: the order the tiles schedule takes tiles in
     int64_t order_min_tiles;  // ... applied to renders of at least this many tiles
     uint32_t* order_hist;  // tile-order bucket counts [kOrderBuckets]: zero between renders
@@ -1124,15 +1132,18 @@ size_t axis_lds_bytes(const MarchArgs& a) {
 }
 
 template <typename GT, int LAYOUT, int OUT, int CAMERA, bool CENSUS, bool SURF>
-void launch_tiles(MarchArgs& a, int rpl, hipStream_t st) {
-    const size_t lds = axis_lds_bytes(a);
+void launch_tiles(MarchArgs& a, const SdfrGrid* g, hipStream_t st) {
+    const int rpl = g->rays_per_lane;
+    size_t lds = axis_lds_bytes(a);
+    if (g->bytes > kCacheResidentBytes && g->lds_per_cu > 0)
+        lds = max(lds, (size_t)g->lds_per_cu / kSpillBlocksPerCU);   // cap the workgroups per CU
     const int per_block = kTileWaves * rpl;
     a.nblocks = (int)((a.logical_tiles + per_block - 1) / per_block);
     // slot packing (fp16 grids, 2 rays per lane, no surf channel): two
     // 64-entry lane lists per wave after the axis tables
     a.pack_off = (a.nx + a.ny + a.nz + 63) & ~63;
     const bool pack = rpl == 2 && !SURF && sizeof(GT) == 2;
-    const size_t lds_pack = pack ? sizeof(uint32_t) * ((size_t)a.pack_off + 128 * kTileWaves) : lds;
+    const size_t lds_pack = pack ? max(lds, sizeof(uint32_t) * ((size_t)a.pack_off + 128 * kTileWaves)) : lds;
     if (rpl == 2)
         march_tiles<GT, LAYOUT, OUT, CAMERA, CENSUS, 2, SURF><<<a.nblocks, 64 * kTileWaves, lds_pack, st>>>(a);
     else
@@ -1182,12 +1193,12 @@ void launch_march(MarchArgs& a, const SdfrGrid* g, bool surf, hipStream_t st) {
         // the surf-mask variant exists for the equiangular camera only
         // (vision.py:463-467) and always runs the tiles schedule
         if constexpr (CAMERA == SDFR_CAM_EQUIANGULAR) {
-            launch_tiles<GT, LAYOUT, OUT, CAMERA, CENSUS, true>(a, g->rays_per_lane, st);
+            launch_tiles<GT, LAYOUT, OUT, CAMERA, CENSUS, true>(a, g, st);
         }
         return;
     }
     if (g->schedule == SDFR_SCHED_TILES) {
-        launch_tiles<GT, LAYOUT, OUT, CAMERA, CENSUS, false>(a, g->rays_per_lane, st);
+        launch_tiles<GT, LAYOUT, OUT, CAMERA, CENSUS, false>(a, g, st);
         return;
     }
     const size_t lds = axis_lds_bytes(a);
@@ -1394,12 +1405,16 @@ SDFR_API SdfrGrid* sdfr_grid_create(const SdfrGridDesc* desc, const void* src, i
     // to HBM, where fewer rays in flight thrash fewer DRAM pages
     g->rays_per_lane = g->bytes > kCacheResidentBytes ? 1 : 2;
     g->cus = 0;
+    g->lds_per_cu = 0;
     g->tile_order = SDFR_ORDER_LOOKAHEAD;
     g->order_min_tiles = kOrderMinTiles;
     g->order_hist = nullptr;
     hipError_t e = hipGetDevice(&g->device);
     if (e == hipSuccess)
         e = hipDeviceGetAttribute(&g->cus, hipDeviceAttributeMultiprocessorCount, g->device);
+    if (e == hipSuccess)
+        e = hipDeviceGetAttribute(&g->lds_per_cu, hipDeviceAttributeMaxSharedMemoryPerMultiprocessor,
+                                  g->device);
 
     const int64_t src_bytes = nvox * (src_dtype == SDFR_F16 ? 2 : 4);
     void* staged = nullptr;
