@@ -98,6 +98,9 @@ constexpr int kTileWaves = 2;
 // spreads cheap regions (sky) and costly ones (grazing ground) evenly over
 // the XCDs, which a contiguous eighth per XCD does not.
 constexpr int kXcdChunk = 64;
+// A voxel byte offset no ray has sampled: real offsets are multiples of
+// the voxel size (2 or 4 bytes).
+constexpr uint32_t kNoVoxel = 0xffffffffu;
 
 // ---------------------------------------------------------------- errors --
 thread_local char g_err[512];
@@ -681,6 +684,12 @@ __global__ __launch_bounds__(64 * kTileWaves) void march_tiles(MarchArgs a) {
     // and inverse_ballot turns it back into the per-lane predicate (the exec
     // mask of the address math and gather), so no vector instruction is spent
     // on bookkeeping. A tile whose rays have all ended skips both.
+    // offset and value of each ray's most recent gather (a march step that
+    // stays in that voxel reads the value again without a gather)
+    uint32_t last_off[RPL];
+    float last_sd[RPL];
+#pragma unroll
+    for (int j = 0; j < RPL; ++j) { last_off[j] = kNoVoxel; last_sd[j] = 0.0f; }
     uint64_t live[RPL];
 #pragma unroll
     for (int j = 0; j < RPL; ++j) live[j] = __builtin_amdgcn_ballot_w64(alive[j]);
@@ -722,6 +731,7 @@ __global__ __launch_bounds__(64 * kTileWaves) void march_tiles(MarchArgs a) {
                 }
                 if (in_f) {
                     dx[0] = mdx; dy[0] = mdy; dz[0] = mdz; t[0] = mt; pix[0] = mpix;
+                    last_off[0] = kNoVoxel;   // the moved ray's next sample is a fresh gather
                     if constexpr (CENSUS) taps[0] = mtaps;
                 }
                 if (in_s) {
@@ -735,7 +745,6 @@ __global__ __launch_bounds__(64 * kTileWaves) void march_tiles(MarchArgs a) {
         float sd[RPL];
 #pragma unroll
         for (int j = 0; j < RPL; ++j) {
-            float s = 0.0f;
             if (__builtin_amdgcn_inverse_ballot_w64(live[j])) {   // ended lanes issue no gather
                 const float px = ex[j] + dx[j] * t[j];
                 const float py = ey[j] + dy[j] * t[j];
@@ -743,9 +752,13 @@ __global__ __launch_bounds__(64 * kTileWaves) void march_tiles(MarchArgs a) {
                 const int ix = (int)__builtin_amdgcn_fmed3f((px - a.mnx) * a.inv_cell, 0.0f, a.fnx1);
                 const int iy = (int)__builtin_amdgcn_fmed3f((py - a.mny) * a.inv_cell, 0.0f, a.fny1);
                 const int iz = (int)__builtin_amdgcn_fmed3f((pz - a.mnz) * a.inv_cell, 0.0f, a.fnz1);
-                s = load_voxel<GT>(rsrc, tab[ix] + tab[a.nx + iy] + tab[a.nx + a.ny + iz]);
+                const uint32_t off = tab[ix] + tab[a.nx + iy] + tab[a.nx + a.ny + iz];
+                // a step that stays in the voxel of the ray's previous sample
+                // reuses that value: same voxel, same sample, one line fewer
+                // for the texture path
+                if (off != last_off[j]) { last_sd[j] = load_voxel<GT>(rsrc, off); last_off[j] = off; }
             }
-            sd[j] = s;
+            sd[j] = last_sd[j];
         }
 #pragma unroll
         for (int j = 0; j < RPL; ++j) {
