@@ -365,9 +365,12 @@ class GpuLidar:
         """The render's ray-table scratch, kept and grown with N. It is
         allocated outside the render call, so a render captured into a graph
         after one eager render of the same N allocates nothing."""
-        need = int(self._lib.sdfr_workspace_bytes(ctypes.byref(cam), n))
-        if need < 0:
-            _sdfr.check(need, "sdfr_workspace_bytes", self._lib)
+        need = self._ws_need.get(n)
+        if need is None:
+            need = int(self._lib.sdfr_workspace_bytes(ctypes.byref(cam), n))
+            if need < 0:
+                _sdfr.check(need, "sdfr_workspace_bytes", self._lib)
+            self._ws_need[n] = need
         ws = getattr(self, "_ws", None)
         if ws is None or ws.numel() < need:
             ws = torch.empty(need, dtype=torch.uint8, device=self.device)
@@ -375,9 +378,16 @@ class GpuLidar:
         return ws
 
     def _cam(self) -> _sdfr.Cam:
-        return _sdfr.Cam(self.W, self.H, self.hfov_deg, self.vfov_deg, self._tan_h, self._tan_v,
-                         self.range, self.near, self.hit_eps, self.min_step, self.max_steps,
-                         _sdfr.CAM_PINHOLE if self.pinhole else _sdfr.CAM_EQUIANGULAR)
+        """The sensor as the C ABI takes it, rebuilt only when an attribute
+        it is made of has changed since the last render (callers may set
+        range, near, max_steps and the like between renders)."""
+        key = (self.W, self.H, self.hfov_deg, self.vfov_deg, self._tan_h, self._tan_v,
+               self.range, self.near, self.hit_eps, self.min_step, self.max_steps, self.pinhole)
+        if key != getattr(self, "_cam_key", None):
+            self._cam_obj = _sdfr.Cam(*key[:-1], _sdfr.CAM_PINHOLE if key[-1] else _sdfr.CAM_EQUIANGULAR)
+            self._cam_key = key
+            self._ws_need = {}   # workspace bytes per N, for this sensor
+        return self._cam_obj
 
     def _f32(self, t, name):
         t = torch.as_tensor(t)
@@ -411,6 +421,14 @@ class GpuLidar:
         return p, (origin, yaw, pitch, ducked)
 
     def _check_out(self, out: torch.Tensor, n: int) -> int:
+        key = (out.shape, out.stride(), out.dtype, out.device, n, self.H, self.W, self.channels)
+        if key == getattr(self, "_out_key", None):
+            return self._out_stride
+        stride = self._check_out_layout(out, n)
+        self._out_key, self._out_stride = key, stride
+        return stride
+
+    def _check_out_layout(self, out: torch.Tensor, n: int) -> int:
         if out.device != self.device or out.dtype not in _OUT_DTYPES:
             raise ValueError("out must be a float32 or bfloat16 tensor on the lidar's device")
         per_env = self.H * self.W * self.channels
@@ -455,11 +473,17 @@ class GpuLidar:
                           taps_ptr)
         cam = self._cam()
         ws = self._workspace(cam, n)
-        with torch.cuda.device(self.device):
+        if torch.cuda.current_device() == self.device.index:
             stream = torch.cuda.current_stream(self.device).cuda_stream
             rc = self._lib.sdfr_render(self._grid, ctypes.byref(cam), ctypes.byref(poses),
                                        ctypes.byref(img), ws.data_ptr(), ws.numel(), stream)
-        _sdfr.check(rc, "sdfr_render", self._lib)
+        else:
+            with torch.cuda.device(self.device):
+                stream = torch.cuda.current_stream(self.device).cuda_stream
+                rc = self._lib.sdfr_render(self._grid, ctypes.byref(cam), ctypes.byref(poses),
+                                           ctypes.byref(img), ws.data_ptr(), ws.numel(), stream)
+        if rc != 0:
+            _sdfr.check(rc, "sdfr_render", self._lib)
         del keep
         return out
 
@@ -474,7 +498,7 @@ class GpuLidar:
         duck = torch.zeros(n, dtype=torch.int32, device=self.device)
         poses, keep = self._poses(zeros, yaw, pitch, duck)
         out = torch.empty(n, self.H, self.W, 3, device=self.device)
-        cam = self._cam()
+        cam = _sdfr.Cam.from_buffer_copy(self._cam())
         if pinhole is not None:
             cam.camera = _sdfr.CAM_PINHOLE if pinhole else _sdfr.CAM_EQUIANGULAR
         with torch.cuda.device(self.device):

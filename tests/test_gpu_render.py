@@ -202,6 +202,35 @@ def test_render_into_an_observation_row(dev):
     assert torch.all(obs[:, :15] == -7.0)
 
 
+def test_settings_changed_between_renders_take_effect(dev):
+    """render keeps the C-ABI camera and the output-layout check of its last
+    call; sensor attributes set between renders, a new output layout and a
+    bad output after a good one must all still be honoured."""
+    w, sc = _scene("small_ramps")
+    ps = w.poses(sc)
+    _say("case settings changed between renders")
+    lid = _lidar(dev, w, sc)
+    want, _ = _oracle(w, sc, ps)
+    assert np.array_equal(_gpu_render(lid, ps, dev).cpu().numpy(), want)
+    lid.max_steps, lid.range, lid.near = 12, 900.0, 600.0
+    want2, _ = _oracle(w, sc, ps, max_steps=12, range_units=900.0, near_range=600.0)
+    assert not np.array_equal(want2, want)
+    assert np.array_equal(_gpu_render(lid, ps, dev).cpu().numpy(), want2)
+    obs = torch.full((len(ps), 15 + w.height * w.width), -7.0, device=dev)
+    _gpu_render(lid, ps, dev, out=obs[:, 15:])
+    assert np.array_equal(obs[:, 15:].reshape(-1, w.height, w.width).cpu().numpy(), want2)
+    with pytest.raises(ValueError):
+        _gpu_render(lid, ps, dev, out=obs[:, 14:])
+    with pytest.raises(ValueError):
+        _gpu_render(lid, ps, dev, out=obs[:, 15:].to(torch.float16))
+    lid.pinhole = True
+    want3, _ = _oracle(w, sc, ps, max_steps=12, range_units=900.0, near_range=600.0,
+                       pinhole=True)
+    assert np.array_equal(_gpu_render(lid, ps, dev).cpu().numpy(), want3)
+    lid.pinhole = False
+    assert np.array_equal(_gpu_render(lid, ps, dev).cpu().numpy(), want2)
+
+
 @pytest.mark.parametrize("W,H", [(9, 5), (33, 33), (1, 1), (128, 64), (20, 12)])
 def test_ray_directions_equal_the_oracle(dev, W, H):
     """sdfr_ray_dirs exposes the march's own ray setup; the oracle restates
