@@ -685,7 +685,10 @@ __global__ __launch_bounds__(64 * kTileWaves) void march_tiles(MarchArgs a) {
     // mask of the address math and gather), so no vector instruction is spent
     // on bookkeeping. A tile whose rays have all ended skips both.
     // offset and value of each ray's most recent gather (a march step that
-    // stays in that voxel reads the value again without a gather)
+    // stays in that voxel reads the value again without a gather). Off where
+    // slot packing is on: vector issue binds there, and the compare and the
+    // kept offset cost more than the gathers they save (~1%).
+    constexpr bool kReuse = !kPack;
     uint32_t last_off[RPL];
     float last_sd[RPL];
 #pragma unroll
@@ -731,7 +734,6 @@ __global__ __launch_bounds__(64 * kTileWaves) void march_tiles(MarchArgs a) {
                 }
                 if (in_f) {
                     dx[0] = mdx; dy[0] = mdy; dz[0] = mdz; t[0] = mt; pix[0] = mpix;
-                    last_off[0] = kNoVoxel;   // the moved ray's next sample is a fresh gather
                     if constexpr (CENSUS) taps[0] = mtaps;
                 }
                 if (in_s) {
@@ -756,7 +758,8 @@ __global__ __launch_bounds__(64 * kTileWaves) void march_tiles(MarchArgs a) {
                 // a step that stays in the voxel of the ray's previous sample
                 // reuses that value: same voxel, same sample, one line fewer
                 // for the texture path
-                if (off != last_off[j]) { last_sd[j] = load_voxel<GT>(rsrc, off); last_off[j] = off; }
+                if constexpr (!kReuse) last_sd[j] = load_voxel<GT>(rsrc, off);
+                else if (off != last_off[j]) { last_sd[j] = load_voxel<GT>(rsrc, off); last_off[j] = off; }
             }
             sd[j] = last_sd[j];
         }
