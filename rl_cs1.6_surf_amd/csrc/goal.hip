@@ -216,16 +216,34 @@ __global__ __launch_bounds__(kThreads) void goal_sweep(GoalArgs a, uint32_t k) {
 }
 
 // reach_max: the largest finite distance (non-negative floats order as their
-// bit patterns).
+// bit patterns). Four distances per load (the distances start the workspace,
+// which the bake requires 64-byte aligned), the last vox % 4 one at a time;
+// one atomic per block (atomics from every wave to the one word serialise).
+constexpr int kReachBlocks = 512;
 __global__ __launch_bounds__(256) void goal_reach_max(const float* d, int64_t vox, uint32_t* best) {
+    __shared__ uint32_t s_m[4];
     uint32_t m = 0;
-    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < vox;
-         i += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t n4 = vox >> 2;
+    const float4* d4 = reinterpret_cast<const float4*>(d);
+    const int64_t step = (int64_t)gridDim.x * blockDim.x;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n4; i += step) {
+        const float4 v = d4[i];
+        if (v.x != INFINITY) m = max(m, __float_as_uint(v.x));
+        if (v.y != INFINITY) m = max(m, __float_as_uint(v.y));
+        if (v.z != INFINITY) m = max(m, __float_as_uint(v.z));
+        if (v.w != INFINITY) m = max(m, __float_as_uint(v.w));
+    }
+    for (int64_t i = (n4 << 2) + (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < vox; i += step) {
         const float v = d[i];
         if (v != INFINITY) m = max(m, __float_as_uint(v));
     }
     for (int off = 32; off > 0; off >>= 1) m = max(m, (uint32_t)__shfl_down(m, off));
-    if ((threadIdx.x & 63) == 0 && m) atomicMax(best, m);
+    if ((threadIdx.x & 63) == 0) s_m[threadIdx.x >> 6] = m;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        m = max(max(s_m[0], s_m[1]), max(s_m[2], s_m[3]));
+        if (m) atomicMax(best, m);
+    }
 }
 
 // +inf -> sentinel, then round(d / quant) clamped to [0, 65535]. The
@@ -398,7 +416,7 @@ SDFR_API int32_t sdfr_goal_bake(const uint8_t* occ, int32_t nx, int32_t ny, int3
         if (host[k % 3u] == 0) done = true;   // k is the next sweep: its queue is empty
     }
     if (!done) return gfail(-7, "sdfr_goal_bake: not converged after %d sweeps", max_sweeps);
-    goal_reach_max<<<1024, 256, 0, st>>>(g.d, L.vox, g.ctl + kReach);
+    goal_reach_max<<<kReachBlocks, 256, 0, st>>>(g.d, L.vox, g.ctl + kReach);
     e = hipGetLastError();
     if (e == hipSuccess) e = hipMemcpyAsync(host, g.ctl, sizeof host, hipMemcpyDeviceToHost, st);
     if (e == hipSuccess) e = hipStreamSynchronize(st);

@@ -541,13 +541,18 @@ def test_persistent_relaunches_reuse_their_counters(dev):
         assert torch.equal(out, full[:n]), n
 
 
-def test_render_inside_a_captured_graph(dev):
+@pytest.mark.parametrize("sort,grid_dtype", [(False, torch.float32), (True, torch.float32),
+                                             (True, torch.float16)])
+def test_render_inside_a_captured_graph(dev, sort, grid_dtype):
     """A hipGraph of one render replays correctly, again and again, with
-    eager work between replays (the kernel clears its own counters)."""
+    eager work between replays (the kernels clear their own counters: the
+    persistent schedule's tile counters, the tile order's bucket counts)."""
     w, sc = _scene("small_ramps")
     ps = w.poses(sc)
-    _say("case graph capture")
-    lid = _lidar(dev, w, sc)
+    _say(f"case graph capture sort={sort} grid={grid_dtype}")
+    lid = _lidar(dev, w, sc, grid_dtype=grid_dtype)
+    if sort:
+        lid.set_tile_order("lookahead", min_tiles=0)   # sort even this small batch
     origin = torch.as_tensor(ps.origin, device=dev)
     yaw = torch.as_tensor(ps.yaw, device=dev)
     pitch = torch.as_tensor(ps.pitch, device=dev)
