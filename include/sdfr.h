@@ -34,7 +34,7 @@ extern "C" {
 
 /* Bumped on every struct or semantic change; the binding refuses a library
  * reporting another value. */
-#define SDFR_ABI_VERSION 8
+#define SDFR_ABI_VERSION 9
 
 /* Element types of caller arrays. */
 enum {
@@ -218,7 +218,7 @@ SDFR_API int32_t sdfr_ray_dirs(const SdfrCam* cam, const SdfrPoses* poses, float
  * device (nonzero = solid); `out` receives nz*ny*nx distances in map units
  * (SDFR_F32 or SDFR_F16, rounded once from fp64), 0 in solid voxels.
  * Bit-identical to the reference's bake for power-of-two cells.
- * `workspace`: sdfr_edt_workspace_bytes() bytes of device memory, 4-byte
+ * `workspace`: sdfr_edt_workspace_bytes() bytes of device memory, 8-byte
  * aligned. Asynchronous on `stream`; 0 or < 0 (sdfr_edt_last_error()). */
 SDFR_API int64_t sdfr_edt_workspace_bytes(int32_t nx, int32_t ny, int32_t nz);
 SDFR_API int32_t sdfr_edt(const uint8_t* occ, int32_t nx, int32_t ny, int32_t nz, float cell,

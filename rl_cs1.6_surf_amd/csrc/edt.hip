@@ -6,11 +6,12 @@
 //
 // Method: the squared distance transform is separable (Felzenszwalb &
 // Huttenlocher, "Distance Transforms of Sampled Functions", 2012). Three
-// passes, one thread per grid line:
-//   x: two sweeps give each voxel its distance to the nearest solid in its
-//      row (the padding makes x = -1 and x = nx solid): g^2;
-//   y: lower envelope of the parabolas f(q) + (y - q)^2 over the column,
-//      with the padded rows q = -1 and q = ny at f = 0;
+// passes:
+//   x: one wave per row: each voxel's distance to the nearest solid in its
+//      row (the padding makes x = -1 and x = nx solid), squared: g^2;
+//   y: one thread per column: lower envelope of the parabolas
+//      f(q) + (y - q)^2 over the column, with the padded rows q = -1 and
+//      q = ny at f = 0;
 //   z: the same along z, then d = sqrt(D * cell^2) in fp64, rounded once.
 // All envelope arithmetic is exact integer arithmetic (squared distances in
 // voxel units fit in int32, intersection comparisons are cross-multiplied in
@@ -19,8 +20,8 @@
 // sum of per-axis squares equals cell^2 * D exactly, so the result is
 // bit-identical to the reference's bake.
 //
-// Scratch: two int32 planes of the grid and one int32 envelope array per
-// line (3 x 4 bytes per voxel, sdfr_edt_workspace_bytes).
+// Scratch: two int32 planes of the grid and one uint64 envelope stack per
+// line (~16 bytes per voxel, sdfr_edt_workspace_bytes).
 
 #include <hip/hip_runtime.h>
 #include <hip/hip_fp16.h>
@@ -54,78 +55,139 @@ __device__ __forceinline__ __half f64_to_f16_rne(double x) {
 }
 
 // Pass x: per row, distance to the nearest solid (pads at -1 and nx), squared.
+// One wave per row; lane l owns the run x in [l*C, (l+1)*C), C = ceil(nx/64).
+// The nearest solid at or left of x is the last solid in the lane's run up to
+// x, else the last solid of any lower lane (a prefix max over the wave), else
+// the pad at -1; the right side mirrors it with a suffix min and the pad at nx.
 __global__ __launch_bounds__(256) void edt_rows(const uint8_t* __restrict__ occ, int32_t* __restrict__ g,
                                                 int nx, int64_t rows) {
-    const int64_t row = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (row >= rows) return;
+    const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (row >= rows) return;   // uniform per wave
+    const int lane = threadIdx.x & 63;
+    const int C = (nx + 63) >> 6;
+    const int x0 = min(lane * C, nx), x1 = min(x0 + C, nx);
     const uint8_t* o = occ + row * nx;
     int32_t* out = g + row * nx;
-    int32_t d = 0;   // distance to the last solid seen, the pad at x = -1 to start
-    for (int x = 0; x < nx; ++x) {
-        d = o[x] ? 0 : d + 1;
-        out[x] = d;
+    int first = nx, last = -1;   // solids in this lane's run
+    for (int x = x0; x < x1; ++x)
+        if (o[x]) {
+            first = min(first, x);
+            last = x;
+        }
+    // inclusive scans over the wave: max of `last` up from lane 0, min of
+    // `first` down from lane 63
+    int lmax = last, rmin = first;
+    for (int off = 1; off < 64; off <<= 1) {
+        const int up = __shfl_up(lmax, off);
+        const int dn = __shfl_down(rmin, off);
+        if (lane >= off) lmax = max(lmax, up);
+        if (lane + off < 64) rmin = min(rmin, dn);
     }
-    d = 0;           // the pad at x = nx
-    for (int x = nx - 1; x >= 0; --x) {
-        d = o[x] ? 0 : d + 1;
-        const int32_t m = out[x] < d ? out[x] : d;
+    int left = __shfl_up(lmax, 1);     // last solid below this lane's run
+    int right = __shfl_down(rmin, 1);  // first solid above it
+    if (lane == 0) left = -1;
+    if (lane == 63) right = nx;
+    for (int x = x0; x < x1; ++x) {
+        if (o[x]) left = x;
+        out[x] = x - left;
+    }
+    for (int x = x1 - 1; x >= x0; --x) {
+        if (o[x]) right = x;
+        const int32_t m = min(out[x], right - x);
         out[x] = m * m;
     }
 }
 
 // One column of the lower-envelope pass. The column has n real samples at
 // stride `stride` from `f`, plus pad samples q = -1 and q = n with value 0.
-// Envelope vertices are stored as q + 1 in v (stride `vstride`).
+// A parabola rooted at p is kept as (p, H) with H = f(p) + p^2, so the
+// intersection of the parabolas rooted at a < b is
+//   s(a, b) = (H_b - H_a) / (2 (b - a)),
+// compared as cross-multiplied int64 fractions (exact). The envelope stack
+// lives in `v` (stride `vstride`), one uint64 per vertex: H << 16 | (p + 1)
+// (H < 2^32 and p + 1 < 2^16 under sdfr_edt's size checks); its top two
+// vertices are kept in registers, so popping one costs a single dependent
+// load, and the next sample is fetched while the current one is placed.
 __device__ __forceinline__ int64_t fval(const int32_t* f, int64_t stride, int n, int q) {
     return (q < 0 || q >= n) ? 0 : (int64_t)f[(int64_t)q * stride];
 }
 
-// Parabola p is left of q's takeover point? The intersection of parabolas
-// rooted at a < b is s(a,b) = ((f_b + b^2) - (f_a + a^2)) / (2(b - a)).
-struct Frac {
-    int64_t num, den;   // den > 0
+struct Vtx {
+    int p;       // root
+    int64_t h;   // f(p) + p^2
 };
 
-__device__ __forceinline__ Frac inter(const int32_t* f, int64_t stride, int n, int a, int b) {
-    Frac s;
-    s.num = (fval(f, stride, n, b) + (int64_t)b * b) - (fval(f, stride, n, a) + (int64_t)a * a);
-    s.den = 2 * (int64_t)(b - a);
-    return s;
+__device__ __forceinline__ uint64_t pack_vtx(Vtx a) {
+    return ((uint64_t)a.h << 16) | (uint64_t)(a.p + 1);
+}
+
+__device__ __forceinline__ Vtx unpack_vtx(uint64_t w) {
+    return Vtx{(int)(w & 0xffffu) - 1, (int64_t)(w >> 16)};
 }
 
 __device__ __forceinline__ void envelope_line(const int32_t* __restrict__ f, int64_t stride, int n,
-                                              int32_t* __restrict__ v, int64_t vstride,
+                                              uint64_t* __restrict__ v, int64_t vstride,
                                               int32_t* __restrict__ out, int64_t ostride,
                                               bool last, float* __restrict__ fout,
                                               __half* __restrict__ hout, double cell2) {
     // build the envelope over q = -1 .. n
-    int k = 0;
-    v[0] = -1 + 1;
-    for (int q = 0; q <= n; ++q) {
-        while (true) {
-            const int p = v[(int64_t)k * vstride] - 1;
-            const Frac s = inter(f, stride, n, p, q);
-            if (k == 0) break;
-            const int pp = v[(int64_t)(k - 1) * vstride] - 1;
-            const Frac zk = inter(f, stride, n, pp, p);
-            // s <= z[k]  <=>  s.num * zk.den <= zk.num * s.den
-            if (s.num * zk.den <= zk.num * s.den) --k;
-            else break;
+    int k = 0;                          // index of the top vertex
+    Vtx top{-1, 1};                     // the pad at q = -1: f = 0
+    Vtx second{0, 0};                   // valid while k >= 1
+    v[0] = pack_vtx(top);
+    // the samples come in chunks of kChunk, the next chunk's loads in flight
+    // while this one is placed (they do not depend on the envelope)
+    constexpr int kChunk = 16;
+    int64_t fc[kChunk], fn[kChunk];
+#pragma unroll
+    for (int i = 0; i < kChunk; ++i) fc[i] = fval(f, stride, n, i);
+    for (int q0 = 0; q0 <= n; q0 += kChunk) {
+#pragma unroll
+        for (int i = 0; i < kChunk; ++i) fn[i] = fval(f, stride, n, q0 + kChunk + i);
+#pragma unroll
+        for (int i = 0; i < kChunk; ++i) {
+            const int q = q0 + i;
+            if (q > n) break;
+            const int64_t hq = fc[i] + (int64_t)q * q;
+            while (k > 0) {
+                // pop the top while q's parabola takes over at or before the
+                // point where the top took over from the vertex below it:
+                // s(top, q) <= s(second, top)
+                const int64_t s_num = hq - top.h, s_den = 2 * (int64_t)(q - top.p);
+                const int64_t z_num = top.h - second.h, z_den = 2 * (int64_t)(top.p - second.p);
+                if (s_num * z_den > z_num * s_den) break;
+                --k;
+                top = second;
+                if (k > 0) second = unpack_vtx(v[(int64_t)(k - 1) * vstride]);
+            }
+            ++k;
+            second = top;
+            top = Vtx{q, hq};
+            v[(int64_t)k * vstride] = pack_vtx(top);
         }
-        ++k;
-        v[(int64_t)k * vstride] = q + 1;
+#pragma unroll
+        for (int i = 0; i < kChunk; ++i) fc[i] = fn[i];
     }
-    // read the envelope at the real samples
+    // read the envelope at the real samples; vertices j .. j+3 in registers
+    // (w[0] current, w[1] next), the later ones loaded ahead of their use
     int j = 0;
+    uint64_t w[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) w[i] = i <= k ? v[(int64_t)i * vstride] : 0;
+    Vtx cur = unpack_vtx(w[0]);
     for (int q = 0; q < n; ++q) {
         while (j < k) {
-            const int a = v[(int64_t)j * vstride] - 1, b = v[(int64_t)(j + 1) * vstride] - 1;
-            const Frac z = inter(f, stride, n, a, b);
-            if (z.num < (int64_t)q * z.den) ++j;   // z[j+1] < q
-            else break;
+            // advance while the next vertex takes over before q: s(cur, nxt) < q
+            const Vtx nxt = unpack_vtx(w[1]);
+            const int64_t z_num = nxt.h - cur.h, z_den = 2 * (int64_t)(nxt.p - cur.p);
+            if (z_num >= (int64_t)q * z_den) break;
+            ++j;
+            cur = nxt;
+            w[1] = w[2];
+            w[2] = w[3];
+            w[3] = j + 3 <= k ? v[(int64_t)(j + 3) * vstride] : 0;
         }
-        const int p = v[(int64_t)j * vstride] - 1;
-        const int64_t d = (int64_t)(q - p) * (q - p) + fval(f, stride, n, p);
+        const int64_t d = (int64_t)(q - cur.p) * (q - cur.p) + (cur.h - (int64_t)cur.p * cur.p);
         if (!last) {
             out[(int64_t)q * ostride] = (int32_t)d;
         } else {
@@ -138,18 +200,18 @@ __device__ __forceinline__ void envelope_line(const int32_t* __restrict__ f, int
 
 // Pass y: one thread per (z, x) column of a [nz][ny][nx] plane array.
 __global__ __launch_bounds__(256) void edt_cols(const int32_t* __restrict__ f, int32_t* __restrict__ out,
-                                                int32_t* __restrict__ v, int nx, int ny, int nz) {
+                                                uint64_t* __restrict__ v, int nx, int ny, int nz) {
     const int64_t line = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     const int64_t lines = (int64_t)nz * nx;
     if (line >= lines) return;
     const int z = (int)(line / nx), x = (int)(line - (int64_t)z * nx);
     const int64_t base = (int64_t)z * ny * nx + x;
-    // envelope scratch: entry j of this line at v[j*lines + line] (coalesced)
+    // envelope stack: entry j of this line at v[j*lines + line] (coalesced)
     envelope_line(f + base, nx, ny, v + line, lines, out + base, nx, false, nullptr, nullptr, 0.0);
 }
 
 // Pass z: one thread per (y, x) line; writes the distances.
-__global__ __launch_bounds__(256) void edt_slabs(const int32_t* __restrict__ f, int32_t* __restrict__ v,
+__global__ __launch_bounds__(256) void edt_slabs(const int32_t* __restrict__ f, uint64_t* __restrict__ v,
                                                  float* __restrict__ fout, __half* __restrict__ hout,
                                                  int nx, int ny, int nz, double cell2) {
     const int64_t line = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -160,12 +222,18 @@ __global__ __launch_bounds__(256) void edt_slabs(const int32_t* __restrict__ f, 
                   fout ? fout + line : nullptr, hout ? hout + line : nullptr, cell2);
 }
 
-int64_t edt_scratch_bytes(int nx, int ny, int nz) {
+// Two int32 planes of the grid, then (8-byte aligned) the uint64 envelope
+// stacks of the longer of the y and z passes.
+int64_t edt_env_offset(int nx, int ny, int nz) {
     const int64_t vox = (int64_t)nx * ny * nz;
+    return (2 * vox * (int64_t)sizeof(int32_t) + 7) & ~(int64_t)7;
+}
+
+int64_t edt_scratch_bytes(int nx, int ny, int nz) {
     const int64_t lines_y = (int64_t)nz * nx, lines_z = (int64_t)ny * nx;
     const int64_t venv = lines_y * (ny + 2) > lines_z * (nz + 2) ? lines_y * (ny + 2)
                                                                  : lines_z * (nz + 2);
-    return (2 * vox + venv) * (int64_t)sizeof(int32_t);
+    return edt_env_offset(nx, ny, nz) + venv * (int64_t)sizeof(uint64_t);
 }
 
 }  // namespace
@@ -198,15 +266,15 @@ SDFR_API int32_t sdfr_edt(const uint8_t* occ, int32_t nx, int32_t ny, int32_t nz
     if (workspace_size < need)
         return efail(-2, "sdfr_edt: workspace of %lld bytes needed (got %lld)", (long long)need,
                      (long long)workspace_size);
-    if (((uintptr_t)workspace & 3u) != 0) return efail(-2, "sdfr_edt: workspace must be 4-byte aligned");
+    if (((uintptr_t)workspace & 7u) != 0) return efail(-2, "sdfr_edt: workspace must be 8-byte aligned");
     const int64_t vox = (int64_t)nx * ny * nz;
     int32_t* a = (int32_t*)workspace;
     int32_t* b = a + vox;
-    int32_t* v = b + vox;
+    uint64_t* v = (uint64_t*)((char*)workspace + edt_env_offset(nx, ny, nz));
     hipStream_t st = (hipStream_t)stream;
     const double cell2 = (double)cell * (double)cell;
     const int64_t rows = (int64_t)nz * ny, cols = (int64_t)nz * nx, lines = (int64_t)ny * nx;
-    edt_rows<<<(int)((rows + 255) / 256), 256, 0, st>>>(occ, a, nx, rows);
+    edt_rows<<<(int)((rows + 3) / 4), 256, 0, st>>>(occ, a, nx, rows);
     edt_cols<<<(int)((cols + 255) / 256), 256, 0, st>>>(a, b, v, nx, ny, nz);
     edt_slabs<<<(int)((lines + 255) / 256), 256, 0, st>>>(
         b, v, out_dtype == SDFR_F32 ? (float*)out : nullptr,

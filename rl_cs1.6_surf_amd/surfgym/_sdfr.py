@@ -18,7 +18,7 @@ import torch  # noqa: F401  (load torch's HIP runtime first, see above)
 PKG_ROOT = Path(__file__).resolve().parents[1]
 LIB_PATH = PKG_ROOT / "lib" / "libsdfr.so"
 
-ABI_VERSION = 8
+ABI_VERSION = 9
 
 # element types (SDFR_* in sdfr.h)
 F32, F16, BF16, I32, I64, U8, F64, U16 = 0, 1, 2, 3, 4, 5, 6, 7
