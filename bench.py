@@ -194,7 +194,7 @@ def _reference_goal_sweeps_torch(occ_dev, cell, lo, hi):
     ops on this GPU: 26 shifted add+minimum passes per sweep over the whole
     grid, solids re-pinned each sweep, a float64 convergence probe every 64
     sweeps, at most 8000 sweeps. Returns (sweeps, seconds). A comparator for
-    the bake's speed, not a checker."""
+    the bake's speed, not a parity reference."""
     import numpy as np
     import torch
     dev = occ_dev.device

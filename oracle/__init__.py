@@ -1,13 +1,13 @@
 """CPU oracle for the SDF depth render — TEST INFRASTRUCTURE ONLY.
 
 Only tests/, ``__graft_entry__.smoke()`` and bench.py's CPU-baseline leg may
-import this package: it is the checker the GPU renderer is measured against,
+import this package: it is the oracle the GPU renderer is measured against,
 never part of the product path.
 
 Restatements of the reference's render (python/surfgym/vision.py) and of
 its goal field:
 
-* :func:`render` — per-ray C loop (``oracle/march.c``), the canonical checker.
+* :func:`render` — per-ray C loop (``oracle/march.c``), the canonical oracle.
   It also returns the number of grid loads each ray issued (the census of
   tools/bench_lidar.py:45-88), which is the algorithmic-bytes count.
 * :mod:`oracle.goal` — the goal-field bake and sampler

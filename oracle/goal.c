@@ -1,5 +1,5 @@
 /* goal.c — CPU restatement of the reference's goal field. TEST
- * INFRASTRUCTURE ONLY: the checker the GPU goal-field bake and sampler are
+ * INFRASTRUCTURE ONLY: the oracle the GPU goal-field bake and sampler are
  * measured against, never part of the product path.
  *
  * oracle_goal_distance and oracle_goal_quantise follow

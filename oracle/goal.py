@@ -3,7 +3,7 @@
 python/surfgym/goalfield.py builds a geodesic distance-to-goal field over the
 free voxels of an occupancy grid (build_goal_field, :159-298) and samples it
 trilinearly over "honest" corners (GoalField.sample, :68-94). This module is
-the checker for the GPU bake and sampler:
+the oracle for the GPU bake and sampler:
 
 * :func:`distance` / :func:`bake` — ``oracle/goal.c``: Dijkstra in fp32 to
   the relaxation's fixpoint, then the sentinel and uint16 quantisation;

@@ -1,6 +1,6 @@
 /* oracle/march.c — CPU restatement of the reference's SDF depth render.
  *
- * TEST INFRASTRUCTURE ONLY. This is the checker the GPU renderer is compared
+ * TEST INFRASTRUCTURE ONLY. This is the oracle the GPU renderer is compared
  * against; only tests/, __graft_entry__.smoke() and bench.py's CPU-baseline
  * leg may load it. The product path never calls it.
  *
