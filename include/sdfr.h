@@ -34,7 +34,7 @@ extern "C" {
 
 /* Bumped on every struct or semantic change; the binding refuses a library
  * reporting another value. */
-#define SDFR_ABI_VERSION 9
+#define SDFR_ABI_VERSION 10
 
 /* Element types of caller arrays. */
 enum {
@@ -177,6 +177,14 @@ SDFR_API int32_t sdfr_grid_set_schedule(SdfrGrid* grid, int32_t schedule, int32_
  * tiles schedule and the surf-mask variant; results do not depend on it.
  * Synchronous; 0 or < 0. No reference counterpart. */
 SDFR_API int32_t sdfr_grid_set_tile_order(SdfrGrid* grid, int32_t order, int64_t min_tiles);
+
+/* Measurement hook, no reference counterpart: with a pair of the caller's
+ * HIP events set (hipEvent_t, both or neither), every later render on this
+ * handle records `start` on its stream right before the march kernel and
+ * `stop` right after it, so hipEventElapsedTime(start, stop) is the march's
+ * own duration (the ray-setup and tile-sort launches fall outside). The
+ * events must stay valid while set; nulls clear them. Synchronous; 0 or < 0. */
+SDFR_API int32_t sdfr_grid_set_march_events(SdfrGrid* grid, void* start, void* stop);
 
 /* Bytes of device memory the handle owns (the re-laid-out grid). */
 SDFR_API int64_t sdfr_grid_bytes(const SdfrGrid* grid);

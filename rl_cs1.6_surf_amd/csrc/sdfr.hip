@@ -135,6 +135,7 @@ struct SdfrGrid {
     int32_t tile_order;    // SDFR_ORDER_*: the order the tiles schedule takes tiles in
     int64_t order_min_tiles;  // ... applied to renders of at least this many tiles
     uint32_t* order_hist;  // tile-order bucket counts [kOrderBuckets]: zero between renders
+    void* march_events[2]; // caller's hipEvent_t pair around the march launch, or nulls
 };
 
 namespace {
@@ -1530,6 +1531,16 @@ SDFR_API int32_t sdfr_grid_set_schedule(SdfrGrid* grid, int32_t schedule, int32_
     return 0;
 }
 
+SDFR_API int32_t sdfr_grid_set_march_events(SdfrGrid* grid, void* start, void* stop) {
+    g_err[0] = '\0';
+    if (!grid) return fail(-1, "sdfr_grid_set_march_events: null grid handle");
+    if ((start == nullptr) != (stop == nullptr))
+        return fail(-2, "sdfr_grid_set_march_events: give both events or neither");
+    grid->march_events[0] = start;
+    grid->march_events[1] = stop;
+    return 0;
+}
+
 SDFR_API int32_t sdfr_grid_set_tile_order(SdfrGrid* grid, int32_t order, int64_t min_tiles) {
     g_err[0] = '\0';
     if (!grid) return fail(-1, "sdfr_grid_set_tile_order: null grid handle");
@@ -1637,6 +1648,9 @@ SDFR_API int32_t sdfr_render(const SdfrGrid* grid, const SdfrCam* cam, const Sdf
         ray_setup<SDFR_CAM_EQUIANGULAR><<<table_blocks + sort_blocks, 256, 0, st>>>(a, table_blocks);
     if (sort_blocks) order_scatter<<<sort_blocks, 256, 0, st>>>(a);
     const bool census = image->taps != nullptr;
+    if (grid->march_events[0] &&
+        hipEventRecord((hipEvent_t)grid->march_events[0], st) != hipSuccess)
+        return fail(-4, "sdfr_render: recording the march start event failed");
     if (grid->store_dtype == SDFR_F16) {
         if (grid->layout == SDFR_LAYOUT_BRICK4)
             dispatch_out<__half, SDFR_LAYOUT_BRICK4>(a, grid, image->dtype, census, surf, st);
@@ -1650,6 +1664,9 @@ SDFR_API int32_t sdfr_render(const SdfrGrid* grid, const SdfrCam* cam, const Sdf
     }
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return fail(-4, "sdfr_render: launch failed: %s", hipGetErrorString(e));
+    if (grid->march_events[1] &&
+        hipEventRecord((hipEvent_t)grid->march_events[1], st) != hipSuccess)
+        return fail(-4, "sdfr_render: recording the march stop event failed");
     return 0;
 }
 

@@ -339,6 +339,13 @@ class GpuLidar:
                     "sdfr_grid_set_tile_order", self._lib)
         self.tile_order = order
 
+    def set_march_events(self, start: int | None, stop: int | None) -> None:
+        """Measurement hook: raw hipEvent_t handles (ints) that every later
+        render records right before and right after its march kernel, on its
+        stream; None, None clears them. The caller owns the events."""
+        _sdfr.check(self._lib.sdfr_grid_set_march_events(self._grid, start, stop),
+                    "sdfr_grid_set_march_events", self._lib)
+
     @classmethod
     def from_grid(cls, sdf, mins, cell, surf_nz=None, **kwargs) -> "GpuLidar":
         """A lidar over an explicit [nz,ny,nx] distance grid (no map core);

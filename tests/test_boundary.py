@@ -104,6 +104,8 @@ def test_schedule_and_tile_order_reject_a_null_handle_without_a_device():
     assert "null grid" in _sdfr.last_error()
     assert lib.sdfr_grid_set_schedule(None, _sdfr.SCHED_TILES, 16, 2) == -1
     assert "null grid" in _sdfr.last_error()
+    assert lib.sdfr_grid_set_march_events(None, None, None) == -1
+    assert "null grid" in _sdfr.last_error()
 
 
 def test_render_rejects_bad_arguments_without_a_device():
