@@ -649,3 +649,42 @@ def test_f16_bricks_against_the_f32_oracle(dev):
          f"depth<=16u {float((d_u <= 16.0).mean()):.6f}")
     assert (d_enc <= ENC_TOL).mean() >= 0.98
     assert (d_u <= 16.0).mean() >= 0.998
+
+
+def test_march_events_time_the_march_alone(dev):
+    """sdfr_grid_set_march_events: the library records the caller's two HIP
+    events around each render's march kernel (bench.py's roofline figure)."""
+    import ctypes
+    w, sc = _scene("ramp_field")
+    ps = w.poses(sc, 256)
+    _say("case march events")
+    lid = _lidar(dev, w, sc)
+    hip = ctypes.CDLL("libamdhip64.so.7")
+    hip.hipEventCreate.argtypes = [ctypes.POINTER(ctypes.c_void_p)]
+    hip.hipEventElapsedTime.argtypes = [ctypes.POINTER(ctypes.c_float), ctypes.c_void_p,
+                                        ctypes.c_void_p]
+    hip.hipEventDestroy.argtypes = [ctypes.c_void_p]
+    ev = [ctypes.c_void_p() for _ in range(2)]
+    for e in ev:
+        assert hip.hipEventCreate(ctypes.byref(e)) == 0
+    try:
+        want = _gpu_render(lid, ps, dev)
+        with pytest.raises(Exception):
+            lid.set_march_events(ev[0].value, None)
+        lid.set_march_events(ev[0].value, ev[1].value)
+        t0 = torch.cuda.Event(enable_timing=True)
+        t1 = torch.cuda.Event(enable_timing=True)
+        t0.record()
+        got = _gpu_render(lid, ps, dev)
+        t1.record()
+        torch.cuda.synchronize()
+        ms = ctypes.c_float()
+        assert hip.hipEventElapsedTime(ctypes.byref(ms), ev[0], ev[1]) == 0
+        assert 0.0 < ms.value <= t0.elapsed_time(t1)
+        assert torch.equal(got, want)
+        lid.set_march_events(None, None)
+        assert torch.equal(_gpu_render(lid, ps, dev), want)
+    finally:
+        torch.cuda.synchronize()
+        for e in ev:
+            hip.hipEventDestroy(e)
