@@ -59,7 +59,7 @@ constexpr int kH = kT + 2;               // tile edge with halo
 constexpr int kHalo = kH * kH * kH;      // 1000 LDS floats
 constexpr int kThreads = kT * kT * kT;   // one thread per tile voxel
 constexpr int kMaxLocal = 96;            // local sweeps per visit; the tile is requeued if hit
-constexpr int kSweepChunk = 8;           // sweeps launched between host checks
+constexpr int kSweepChunk = 32;          // sweeps launched between host checks
 
 // control words after the queues (uint32)
 enum { kCount0 = 0, kCount1 = 1, kCount2 = 2, kSeeds = 3, kReach = 4, kLastBusy = 5, kVisitsLo = 6,
