@@ -445,7 +445,8 @@ def main(argv=None):
             f"{statistics.median(march_ms) * 1e3:.1f} us" if march_ms else ""))
 
     copy_gbs = None if args.no_copy else copy_bandwidth(dev)
-    traffic = profiled_traffic(f"{w.name} {args.schedule} rpl={lid.rays_per_lane} {args.layout} {w.store}"
+    rpl = lid.effective_rays_per_lane(n)
+    traffic = profiled_traffic(f"{w.name} {args.schedule} rpl={rpl} {args.layout} {w.store}"
                                f" order={lid.tile_order}")
     if copy_gbs:
         _log(f"[bench] device copy {copy_gbs:.0f} GB/s")
@@ -465,7 +466,7 @@ def main(argv=None):
         "config": {"workload": w.name, "envs": n, "image": f"{w.width}x{w.height}",
                    "rays": rays, "grid": f"{sc.nx}x{sc.ny}x{sc.nz} {w.store} @{sc.cell:g}u",
                    "layout": args.layout, "schedule": args.schedule, "refill_lanes": args.refill,
-                   "rays_per_lane": lid.rays_per_lane, "tile_order": lid.tile_order,
+                   "rays_per_lane": rpl, "tile_order": lid.tile_order,
                    "out": w.out_dtype, "max_steps": w.max_steps,
                    "hit_eps": w.hit_eps, "range": round(w.range_units, 3),
                    "near": round(w.near_range, 3), "grid_loads_per_ray": round(loads / rays, 4),

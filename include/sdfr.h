@@ -34,7 +34,7 @@ extern "C" {
 
 /* Bumped on every struct or semantic change; the binding refuses a library
  * reporting another value. */
-#define SDFR_ABI_VERSION 10
+#define SDFR_ABI_VERSION 11
 
 /* Element types of caller arrays. */
 enum {
@@ -161,13 +161,21 @@ SDFR_API int32_t sdfr_grid_attach_surfnz(SdfrGrid* grid, const void* src, int32_
  * SDFR_SCHED_* value (default SDFR_SCHED_TILES); `refill_lanes` (1..64,
  * default 16) is the number of free lanes at which a persistent wave takes
  * new rays; `rays_per_lane` is how many tiles a wave marches at once: 1 or
- * 2 (default 2) for the tiles schedule, 1..4 slots for the slots schedule.
+ * 2 for the tiles schedule, 1..4 slots for the slots schedule, or 0 (the
+ * default) to let each render choose: 1 for grids above 192 MiB and for
+ * renders of fewer than 65536 tiles (512 envs of 128x64), else 2.
  * Surf-mask renders always use the tiles schedule. Results do not depend
  * on any of them. Synchronous; 0 or < 0. No reference counterpart: the
  * Triton launch has one fixed shape (vision.py:48-54; tools/proto_march.py
  * sweeps it). */
 SDFR_API int32_t sdfr_grid_set_schedule(SdfrGrid* grid, int32_t schedule, int32_t refill_lanes,
                                         int32_t rays_per_lane);
+
+/* The rays per lane (tiles schedule) or slots per wave (slots schedule) a
+ * render of `n_envs` images of `cam` would run with on this handle; < 0 on
+ * bad arguments. No reference counterpart. */
+SDFR_API int32_t sdfr_render_rays_per_lane(const SdfrGrid* grid, const SdfrCam* cam,
+                                           int32_t n_envs);
 
 /* Chooses the tile order of later renders on this handle (SDFR_ORDER_*,
  * default SDFR_ORDER_LOOKAHEAD). The lookahead order costs two small sort

@@ -101,6 +101,12 @@ constexpr int kXcdChunk = 64;
 // A voxel byte offset no ray has sampled: real offsets are multiples of
 // the voxel size (2 or 4 bytes).
 constexpr uint32_t kNoVoxel = 0xffffffffu;
+// Rays per lane by render size (a handle left at rays_per_lane 0): renders
+// of fewer tiles than this are latency-bound (few rounds of waves, the
+// longest rays' step chains set the time), and one tile per wave halves each
+// wave's instructions per step: 16-20% faster at 1-16 envs of 128x64, 5% at
+// 256; equal at 512, beyond which two tiles per wave win.
+constexpr int64_t kSmallRenderTiles = 1 << 16;
 
 // ---------------------------------------------------------------- errors --
 thread_local char g_err[512];
@@ -126,7 +132,7 @@ struct SdfrGrid {
     uint32_t* counters;    // persistent schedule: tile claim counters + exit counter
     int32_t schedule;      // SDFR_SCHED_*
     int32_t refill_lanes;  // persistent schedule: refill when this many lanes are free
-    int32_t rays_per_lane; // tiles schedule: rays each lane marches at once (1, 2)
+    int32_t rays_per_lane; // tiles: rays each lane marches at once (1, 2; 0 = by render size)
     void* nz_data;         // surf mask grid (int8), same layout as data, or null
     int64_t nz_bytes;
     int device;
@@ -270,6 +276,7 @@ struct MarchArgs {
     uint32_t* order_rank;         // place of each unit within its bucket
     int order_shift;              // voxel index >> shift = tile-order cell
     float lookahead;              // distance along a unit's centre ray that keys it
+    int rpl;                      // this render's rays per lane (tiles) or slots per wave
     int order_unit;               // tiles per sorted unit: one workgroup's, kTileWaves * RPL
     int pack_off;                 // tiles schedule: word offset of the packing lane lists in LDS
     int64_t order_units;          // units the order sorts
@@ -1148,9 +1155,18 @@ size_t axis_lds_bytes(const MarchArgs& a) {
     return sizeof(uint32_t) * (size_t)(a.nx + a.ny + a.nz);
 }
 
+// The rays per lane (tiles) or slots per wave (slots) a render of `tiles`
+// 8x8 tiles runs with: the handle's setting, or by default 1 for grids
+// beyond the Infinity Cache (fewer rays in flight, fewer misses) and for
+// small renders, else 2.
+int render_rpl(const SdfrGrid* g, int64_t tiles) {
+    if (g->rays_per_lane > 0) return g->rays_per_lane;
+    return (g->bytes > kCacheResidentBytes || tiles < kSmallRenderTiles) ? 1 : 2;
+}
+
 template <typename GT, int LAYOUT, int OUT, int CAMERA, bool CENSUS, bool SURF>
 void launch_tiles(MarchArgs& a, const SdfrGrid* g, hipStream_t st) {
-    const int rpl = g->rays_per_lane;
+    const int rpl = a.rpl;
     size_t lds = axis_lds_bytes(a);
     if (g->bytes > kCacheResidentBytes && g->lds_per_cu > 0)
         lds = max(lds, (size_t)g->lds_per_cu / kSpillBlocksPerCU);   // cap the workgroups per CU
@@ -1184,7 +1200,7 @@ int persistent_blocks(K kernel, const MarchArgs& a, const SdfrGrid* g, size_t ld
 
 template <typename GT, int LAYOUT, int OUT, int CAMERA, bool CENSUS>
 void launch_slots(MarchArgs& a, const SdfrGrid* g, size_t lds, hipStream_t st) {
-    switch (g->rays_per_lane) {
+    switch (a.rpl) {
     case 1:
         a.nblocks = persistent_blocks(march_slots<GT, LAYOUT, OUT, CAMERA, CENSUS, 1>, a, g, lds, 1);
         march_slots<GT, LAYOUT, OUT, CAMERA, CENSUS, 1><<<a.nblocks, 256, lds, st>>>(a);
@@ -1420,7 +1436,7 @@ SDFR_API SdfrGrid* sdfr_grid_create(const SdfrGridDesc* desc, const void* src, i
     g->refill_lanes = 16;
     // two tiles per wave while the grid is cache-resident; one when it spills
     // to HBM, where fewer rays in flight thrash fewer DRAM pages
-    g->rays_per_lane = g->bytes > kCacheResidentBytes ? 1 : 2;
+    g->rays_per_lane = 0;   // by grid and render size
     g->cus = 0;
     g->lds_per_cu = 0;
     g->tile_order = SDFR_ORDER_LOOKAHEAD;
@@ -1522,13 +1538,23 @@ SDFR_API int32_t sdfr_grid_set_schedule(SdfrGrid* grid, int32_t schedule, int32_
         return fail(-2, "sdfr_grid_set_schedule: refill_lanes must be in 1..64 (got %d)",
                     refill_lanes);
     const int max_rpl = schedule == SDFR_SCHED_SLOTS ? 4 : 2;
-    if (rays_per_lane < 1 || rays_per_lane > max_rpl)
-        return fail(-2, "sdfr_grid_set_schedule: rays_per_lane must be in 1..%d for this schedule "
-                    "(got %d)", max_rpl, rays_per_lane);
+    if (rays_per_lane < 0 || rays_per_lane > max_rpl)
+        return fail(-2, "sdfr_grid_set_schedule: rays_per_lane must be in 0..%d for this schedule "
+                    "(got %d; 0 = by grid and render size)", max_rpl, rays_per_lane);
     grid->schedule = schedule;
     grid->refill_lanes = refill_lanes;
     grid->rays_per_lane = rays_per_lane;
     return 0;
+}
+
+SDFR_API int32_t sdfr_render_rays_per_lane(const SdfrGrid* grid, const SdfrCam* cam,
+                                           int32_t n_envs) {
+    g_err[0] = '\0';
+    if (!grid) return fail(-1, "sdfr_render_rays_per_lane: null grid handle");
+    if (!cam || cam->width < 1 || cam->height < 1 || n_envs < 1)
+        return fail(-2, "sdfr_render_rays_per_lane: need a camera with positive size and n_envs >= 1");
+    const int64_t tiles = (int64_t)((cam->width + 7) / 8) * ((cam->height + 7) / 8) * n_envs;
+    return render_rpl(grid, tiles);
 }
 
 SDFR_API int32_t sdfr_grid_set_march_events(SdfrGrid* grid, void* start, void* stop) {
@@ -1621,7 +1647,8 @@ SDFR_API int32_t sdfr_render(const SdfrGrid* grid, const SdfrCam* cam, const Sdf
     a.order_rank = nullptr;
     a.order_shift = 0;
     a.lookahead = kOrderLookahead * cam->near;
-    a.order_unit = kTileWaves * grid->rays_per_lane;
+    a.rpl = render_rpl(grid, a.total_tiles);
+    a.order_unit = kTileWaves * a.rpl;
     a.order_units = (a.total_tiles + a.order_unit - 1) / a.order_unit;
     a.logical_tiles = a.total_tiles;
     if (grid->tile_order == SDFR_ORDER_LOOKAHEAD && (grid->schedule == SDFR_SCHED_TILES || surf) &&

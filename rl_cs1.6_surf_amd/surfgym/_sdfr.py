@@ -18,7 +18,7 @@ import torch  # noqa: F401  (load torch's HIP runtime first, see above)
 PKG_ROOT = Path(__file__).resolve().parents[1]
 LIB_PATH = PKG_ROOT / "lib" / "libsdfr.so"
 
-ABI_VERSION = 10
+ABI_VERSION = 11
 
 # element types (SDFR_* in sdfr.h)
 F32, F16, BF16, I32, I64, U8, F64, U16 = 0, 1, 2, 3, 4, 5, 6, 7
@@ -29,7 +29,7 @@ ORDER_LAUNCH, ORDER_LOOKAHEAD = 0, 1
 
 EXPORTS = ("sdfr_abi_version", "sdfr_last_error", "sdfr_grid_create", "sdfr_grid_destroy",
            "sdfr_grid_bytes", "sdfr_grid_attach_surfnz", "sdfr_grid_set_schedule",
-           "sdfr_grid_set_tile_order", "sdfr_grid_set_march_events",
+           "sdfr_grid_set_tile_order", "sdfr_grid_set_march_events", "sdfr_render_rays_per_lane",
            "sdfr_workspace_bytes", "sdfr_render", "sdfr_ray_dirs", "sdfr_edt_workspace_bytes",
            "sdfr_edt", "sdfr_edt_last_error", "sdfr_goal_workspace_bytes", "sdfr_goal_bake",
            "sdfr_goal_sample", "sdfr_goal_last_error")
@@ -105,6 +105,8 @@ def load(path: Path | str | None = None):
     lib.sdfr_grid_set_tile_order.restype = i32
     lib.sdfr_grid_set_tile_order.argtypes = [vp, i32, i64]
     lib.sdfr_grid_set_march_events.restype = i32
+    lib.sdfr_render_rays_per_lane.restype = i32
+    lib.sdfr_render_rays_per_lane.argtypes = [vp, ctypes.POINTER(Cam), i32]
     lib.sdfr_grid_set_march_events.argtypes = [vp, vp, vp]
     lib.sdfr_workspace_bytes.restype = i64
     lib.sdfr_workspace_bytes.argtypes = [ctypes.POINTER(Cam), i32]

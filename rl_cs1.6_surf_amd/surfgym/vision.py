@@ -191,8 +191,10 @@ class GpuLidar:
       0.3*cell by default (vision.py:87-88);
     * ``schedule`` / ``refill_lanes`` / ``rays_per_lane`` — how the kernel
       schedules rays: launch-scheduled waves of 8x8 pixel "tiles", each lane
-      marching ``rays_per_lane`` rays at once (default: 2 for grids that fit
-      the Infinity Cache, 1 above 192 MiB); "slots", persistent waves holding
+      marching ``rays_per_lane`` rays at once (default None: each render
+      picks 1 for grids above 192 MiB and for renders under 512 envs of
+      128x64, else 2; see :meth:`effective_rays_per_lane`); "slots",
+      persistent waves holding
       ``rays_per_lane`` (1-4) tiles that each take a new tile when their 64
       rays end; or "persistent" waves that refill lanes with new rays once
       ``refill_lanes`` of them have finished. The results are identical;
@@ -310,17 +312,26 @@ class GpuLidar:
     def set_schedule(self, schedule: str = "tiles", refill_lanes: int = 16,
                      rays_per_lane: int | None = None) -> None:
         """Switch the ray schedule of later renders (results are unchanged).
-        ``rays_per_lane=None`` picks 2 while the grid fits the Infinity Cache
-        and 1 above 192 MiB, as the library does for a new grid."""
-        if rays_per_lane is None:
-            rays_per_lane = 1 if self.grid_bytes > (192 << 20) else 2
+        ``rays_per_lane=None`` lets each render choose (the library's
+        default: 1 for grids above 192 MiB and for renders of fewer than
+        65536 8x8 tiles, else 2); ``rays_per_lane`` then reads None."""
         if schedule not in _SCHEDULES:
             raise ValueError(f"schedule must be one of {sorted(_SCHEDULES)}, got {schedule!r}")
+        rpl = 0 if rays_per_lane is None else int(rays_per_lane)
         _sdfr.check(self._lib.sdfr_grid_set_schedule(self._grid, _SCHEDULES[schedule],
-                                                     int(refill_lanes), int(rays_per_lane)),
+                                                     int(refill_lanes), rpl),
                     "sdfr_grid_set_schedule", self._lib)
         self.schedule, self.refill_lanes = schedule, int(refill_lanes)
-        self.rays_per_lane = int(rays_per_lane)
+        self.rays_per_lane = None if rays_per_lane is None else rpl
+
+    def effective_rays_per_lane(self, n_envs: int) -> int:
+        """Rays per lane (tiles schedule) or slots per wave (slots schedule)
+        a render of ``n_envs`` images runs with."""
+        r = int(self._lib.sdfr_render_rays_per_lane(self._grid, ctypes.byref(self._cam()),
+                                                    int(n_envs)))
+        if r < 0:
+            _sdfr.check(r, "sdfr_render_rays_per_lane", self._lib)
+        return r
 
     def set_tile_order(self, order: str = "lookahead", min_tiles: int | None = None) -> None:
         """The order the tiles schedule takes 8x8 pixel tiles in: "launch"

@@ -95,12 +95,14 @@ def test_small_ramps_matches_the_oracle(dev, layout):
     assert (taps.cpu().numpy()[ok] == loads[ok]).mean() > 0.999
 
 
-@pytest.mark.parametrize("layout", ["linear", "brick4"])
-def test_ramp_field_matches_the_oracle(dev, layout):
+@pytest.mark.parametrize("layout,rpl", [("linear", None), ("brick4", None), ("brick4", 2)])
+def test_ramp_field_matches_the_oracle(dev, layout, rpl):
+    """256 envs: one ray per lane by default (a small render), and two."""
     w, sc = _scene("ramp_field")
     ps = w.poses(sc, 256)
-    _say(f"case ramp_field layout={layout} envs={len(ps)}")
-    lid = _lidar(dev, w, sc, layout=layout)
+    _say(f"case ramp_field layout={layout} rpl={rpl} envs={len(ps)}")
+    lid = _lidar(dev, w, sc, layout=layout, rays_per_lane=rpl)
+    assert lid.effective_rays_per_lane(len(ps)) == (rpl or 1)
     got = _gpu_render(lid, ps, dev).cpu().numpy()
     want, _ = _oracle(w, sc, ps)
     _assert_parity(got, want, w, f"ramp_field/{layout}")
@@ -131,8 +133,8 @@ def test_f16_slot_packing_is_exact(dev, name, n, size):
     ps = w.poses(sc, n)
     W, H = size if size else (w.width, w.height)
     _say(f"case f16 packing {name} n={n} {W}x{H}")
-    lid = _lidar(dev, w, sc, grid_dtype=torch.float16, width=W, height=H)
-    assert lid.rays_per_lane == 2
+    lid = _lidar(dev, w, sc, grid_dtype=torch.float16, width=W, height=H, rays_per_lane=2)
+    assert lid.rays_per_lane == 2 and lid.effective_rays_per_lane(n) == 2
     want, want_taps = _oracle(w, sc, ps, store="f16", width=W, height=H)
     for order in ("lookahead", "launch"):
         lid.set_tile_order(order, min_tiles=0)
@@ -427,9 +429,16 @@ def test_schedule_arguments_are_checked(dev):
     from surfgym import _sdfr
     w, sc = _scene("small_ramps")
     lid = _lidar(dev, w, sc)
-    assert lid.rays_per_lane == 2             # a cache-resident grid
+    # by render size on a cache-resident grid: one ray per lane below 65536
+    # tiles (512 envs of 128x64), two from there on
+    assert lid.rays_per_lane is None
+    assert [lid.effective_rays_per_lane(n) for n in (1, 16, 511, 512, 2048)] == [1, 1, 1, 2, 2]
+    lid.set_schedule("tiles", rays_per_lane=2)
+    assert lid.rays_per_lane == 2 and lid.effective_rays_per_lane(1) == 2
     with pytest.raises(_sdfr.SdfrError, match="rays_per_lane"):
         lid.set_schedule("tiles", rays_per_lane=3)
+    with pytest.raises(_sdfr.SdfrError, match="rays_per_lane"):
+        lid.set_schedule("tiles", rays_per_lane=-1)
     with pytest.raises(_sdfr.SdfrError, match="rays_per_lane"):
         lid.set_schedule("slots", rays_per_lane=5)
     with pytest.raises(_sdfr.SdfrError, match="refill_lanes"):
@@ -440,16 +449,17 @@ def test_schedule_arguments_are_checked(dev):
     assert (lid.schedule, lid.rays_per_lane) == ("slots", 4)
 
 
-@pytest.mark.parametrize("name,n", [("ramp_field", 256), ("winding_track", 64), ("small_ramps", 16)])
-def test_tile_order_is_a_permutation_and_changes_nothing(dev, name, n):
+@pytest.mark.parametrize("name,n,rpl", [("ramp_field", 256, None), ("ramp_field", 256, 2),
+                                        ("winding_track", 64, None), ("small_ramps", 16, 2)])
+def test_tile_order_is_a_permutation_and_changes_nothing(dev, name, n, rpl):
     """The lookahead tile order (default) sorts the tiles in runs of one
     workgroup's tiles (two waves x rays per lane); the sorted list in the
     workspace is a permutation of all runs, and images and censuses are
     bit-identical to env-order launches."""
     w, sc = _scene(name)
     ps = w.poses(sc, n)
-    _say(f"case tile order {name} n={n}")
-    lid = _lidar(dev, w, sc)
+    _say(f"case tile order {name} n={n} rpl={rpl}")
+    lid = _lidar(dev, w, sc, rays_per_lane=rpl)
     assert lid.tile_order == "lookahead"
     lid.set_tile_order("lookahead", min_tiles=0)      # sort however small the render
     # a tile the sorted schedule never marched would keep these fills
@@ -458,7 +468,7 @@ def test_tile_order_is_a_permutation_and_changes_nothing(dev, name, n):
     _gpu_render(lid, ps, dev, taps=ta, out=a)
     torch.cuda.synchronize()
     tiles = n * (w.width // 8) * (w.height // 8)
-    unit = 2 * lid.rays_per_lane
+    unit = 2 * lid.effective_rays_per_lane(n)
     units = (tiles + unit - 1) // unit
     rt_bytes = -(-(n * (w.width + w.height + 4) * 8) // 256) * 256
     perm = lid._ws[rt_bytes:rt_bytes + 4 * units].view(torch.int32).cpu().numpy()
@@ -486,7 +496,7 @@ def test_small_renders_skip_the_sort_by_default(dev):
     tiles = n * (w.width // 8) * (w.height // 8)
     rt_bytes = -(-(n * (w.width + w.height + 4) * 8) // 256) * 256
     want = _gpu_render(lid, ps, dev).clone()
-    units = tiles // (2 * lid.rays_per_lane)
+    units = tiles // (2 * lid.effective_rays_per_lane(n))
     for min_tiles, sorted_ in ((None, False), (tiles + 1, False), (tiles, True), (0, True)):
         lid.set_tile_order("lookahead", min_tiles=min_tiles)
         lid._ws[rt_bytes:rt_bytes + 4 * units].fill_(255)       # perm slots read -1
@@ -606,7 +616,8 @@ def test_winding_track_matches_the_oracle(dev):
     ps = w.poses(sc, 96)
     _say(f"case winding_track envs={len(ps)}")
     lid = _lidar(dev, w, sc)
-    assert lid.rays_per_lane == 1          # a grid beyond the Infinity Cache: one tile per wave
+    # a grid beyond the Infinity Cache: one tile per wave at any batch size
+    assert lid.effective_rays_per_lane(len(ps)) == 1 and lid.effective_rays_per_lane(2048) == 1
     got = _gpu_render(lid, ps, dev).cpu().numpy()
     want, _ = _oracle(w, sc, ps)
     _assert_parity(got, want, w, "winding_track")
