@@ -174,6 +174,18 @@ def _ducked_code(t: torch.Tensor) -> int:
     return _DUCK_DTYPES.get(t.dtype, -1)
 
 
+# The current stream's raw handle for a device index: torch's own accessor
+# (what torch.cuda.current_stream(...).cuda_stream reads, without building a
+# Stream object per call), else the public route.
+_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
+def _current_stream(device: torch.device) -> int:
+    if _raw_stream is not None:
+        return _raw_stream(device.index)
+    return torch.cuda.current_stream(device).cuda_stream
+
+
 class GpuLidar:
     """Batched depth-image renderer over a voxel SDF.
 
@@ -414,7 +426,10 @@ class GpuLidar:
         return t
 
     def _poses(self, origin, yaw_deg, pitch_deg, ducked):
-        origin = self._f32(origin, "origin")
+        dev = self.device
+        if not (isinstance(origin, torch.Tensor) and origin.dtype == torch.float32
+                and origin.device == dev):
+            origin = self._f32(origin, "origin")
         if origin.dim() != 2 or origin.shape[1] != 3:
             raise ValueError(f"origin must be (N, 3), got {tuple(origin.shape)}")
         if origin.stride(1) != 1:
@@ -422,12 +437,20 @@ class GpuLidar:
         n = origin.shape[0]
         if n < 1:
             raise ValueError("render needs at least one env")
-        yaw = self._f32(yaw_deg, "yaw_deg").reshape(-1)
-        pitch = self._f32(pitch_deg, "pitch_deg").reshape(-1)
-        ducked = torch.as_tensor(ducked)
-        if ducked.device != self.device:
-            ducked = ducked.to(self.device)
-        ducked = ducked.reshape(-1)
+        yaw, pitch = yaw_deg, pitch_deg
+        if not (isinstance(yaw, torch.Tensor) and yaw.dtype == torch.float32 and yaw.device == dev):
+            yaw = self._f32(yaw, "yaw_deg")
+        if not (isinstance(pitch, torch.Tensor) and pitch.dtype == torch.float32
+                and pitch.device == dev):
+            pitch = self._f32(pitch, "pitch_deg")
+        if yaw.dim() != 1:
+            yaw = yaw.reshape(-1)
+        if pitch.dim() != 1:
+            pitch = pitch.reshape(-1)
+        if not (isinstance(ducked, torch.Tensor) and ducked.device == dev):
+            ducked = torch.as_tensor(ducked).to(dev)
+        if ducked.dim() != 1:
+            ducked = ducked.reshape(-1)
         if _ducked_code(ducked) < 0:
             ducked = ducked.to(torch.int32)
         for name, t in (("yaw_deg", yaw), ("pitch_deg", pitch), ("ducked", ducked)):
@@ -463,7 +486,8 @@ class GpuLidar:
         return out.stride(0) if n > 1 else per_env
 
     # ---------------------------------------------------------------- render --
-    @torch.no_grad()
+    # (no autograd context: the inputs are read by pointer and the output is
+    # a fresh tensor without a graph either way)
     def render(self, origin, yaw_deg, pitch_deg, ducked, out=None, taps=None):
         """origin (N,3), yaw/pitch (N,) degrees, ducked (N,) bool/int/float ->
         (N, H, W) float32 depth encodings, or (N, H, W, 2) (depth, |n_z|)
@@ -492,14 +516,14 @@ class GpuLidar:
         cam = self._cam()
         ws = self._workspace(cam, n)
         if torch.cuda.current_device() == self.device.index:
-            stream = torch.cuda.current_stream(self.device).cuda_stream
             rc = self._lib.sdfr_render(self._grid, ctypes.byref(cam), ctypes.byref(poses),
-                                       ctypes.byref(img), ws.data_ptr(), ws.numel(), stream)
+                                       ctypes.byref(img), ws.data_ptr(), ws.numel(),
+                                       _current_stream(self.device))
         else:
             with torch.cuda.device(self.device):
-                stream = torch.cuda.current_stream(self.device).cuda_stream
                 rc = self._lib.sdfr_render(self._grid, ctypes.byref(cam), ctypes.byref(poses),
-                                           ctypes.byref(img), ws.data_ptr(), ws.numel(), stream)
+                                           ctypes.byref(img), ws.data_ptr(), ws.numel(),
+                                           _current_stream(self.device))
         if rc != 0:
             _sdfr.check(rc, "sdfr_render", self._lib)
         del keep
