@@ -32,7 +32,8 @@
 //      writes the sorted list (see "tile order");
 //   2. the march, in one of three schedules with identical results:
 //      - tiles (default): launch-scheduled two-wave workgroups, each wave
-//        marching 8x8 pixel tiles with RPL rays per lane in flight at once;
+//        marching RPL 8x8 pixel tiles at once, RPL rays per lane (1 or 2,
+//        chosen per render by render_rpl unless the caller fixes it);
 //      - persistent: a grid that fills the GPU once; each wave keeps 64 ray
 //        slots and refills finished slots with new rays (ray compaction),
 //        pulling 8x8 pixel tiles from per-XCD work counters. It keeps every
