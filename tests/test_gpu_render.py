@@ -699,3 +699,28 @@ def test_march_events_time_the_march_alone(dev):
         torch.cuda.synchronize()
         for e in ev:
             hip.hipEventDestroy(e)
+
+
+def test_two_lidars_on_two_streams_at_once(dev):
+    """Handles share no state: two lidars (each with its own bucket counts,
+    counters and workspace) rendering sorted batches on two streams at the
+    same time give the images each gives alone."""
+    w, sc = _scene("small_ramps")
+    ps = w.poses(sc)
+    _say("case two streams")
+    lids = [_lidar(dev, w, sc), _lidar(dev, w, sc, schedule="persistent")]
+    for lid in lids:
+        lid.set_tile_order("lookahead", min_tiles=0)
+    args = [torch.as_tensor(v, device=dev) for v in (ps.origin, ps.yaw, ps.pitch, ps.ducked)]
+    shifted = [args[0], args[1] + 90.0, args[2], args[3]]
+    want = [lids[0].render(*args).clone(), lids[1].render(*shifted).clone()]
+    streams = [torch.cuda.Stream(device=dev) for _ in lids]
+    outs = [torch.empty_like(want[0]) for _ in lids]
+    torch.cuda.synchronize()
+    for _ in range(8):
+        for lid, st, a, o in zip(lids, streams, (args, shifted), outs):
+            with torch.cuda.stream(st):
+                o.fill_(-1.0)
+                lid.render(*a, out=o)
+        torch.cuda.synchronize()
+        assert torch.equal(outs[0], want[0]) and torch.equal(outs[1], want[1])
