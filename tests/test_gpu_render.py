@@ -724,3 +724,25 @@ def test_two_lidars_on_two_streams_at_once(dev):
                 lid.render(*a, out=o)
         torch.cuda.synchronize()
         assert torch.equal(outs[0], want[0]) and torch.equal(outs[1], want[1])
+
+
+@pytest.mark.parametrize("name", ["winding_track", "sparse_grazing", "ramp_field_f16_bf16"])
+def test_bench_configurations_are_bit_exact_at_full_size(dev, name):
+    """Each bench.py workload at its full size and default schedule (tile
+    order, rays per lane, occupancy cap, slot packing): every encoding equals
+    the oracle's bit for bit (on the f16-rounded grid for the fp16 bricks,
+    then rounded to bf16 as the bf16 output is)."""
+    w, sc = _scene(name)
+    ps = w.poses(sc)
+    f16 = w.store == "f16"
+    _say(f"case full-size {name} envs={len(ps)}")
+    lid = _lidar(dev, w, sc, grid_dtype=torch.float16 if f16 else torch.float32)
+    odt = torch.bfloat16 if w.out_dtype == "bf16" else torch.float32
+    out = torch.empty(len(ps), 1, w.height, w.width, dtype=odt, device=dev)
+    _gpu_render(lid, ps, dev, out=out)
+    want, _ = _oracle(w, sc, ps, store=w.store)
+    want_t = torch.as_tensor(want).reshape(out.shape).to(odt)
+    got = out.cpu()
+    exact = float((got == want_t).float().mean())
+    _say(f"{name}: {got.numel()} rays, exact {exact:.6f}")
+    assert torch.equal(got, want_t)
