@@ -281,6 +281,60 @@ def test_march_invariants_on_a_ramp_scene():
             sc.grid_value((p + d * 1e-2)[None])[0] <= w.hit_eps
 
 
+def _remarch_f64(grid, mins, cell, eye, yaw_deg, pitch_deg, W, H, rng, near, eps, mstep, steps):
+    """A float64 sphere trace of one env written from the algorithm's
+    statement, not from the oracle: view rotations as matrices, nearest
+    voxel by floor, the stop rule and the encoding as the reference states
+    them (vision.py:59-116)."""
+    nz, ny, nx = grid.shape
+    img = np.empty((H, W))
+    for r in range(H):
+        for c in range(W):
+            yw = math.radians(yaw_deg) + math.radians(120.0 * (0.5 - (c + 0.5) / W))
+            pt = math.radians(pitch_deg) + math.radians(90.0 * (0.5 - (r + 0.5) / H))
+            rz = np.array([[math.cos(yw), -math.sin(yw), 0], [math.sin(yw), math.cos(yw), 0],
+                           [0, 0, 1]])
+            ry = np.array([[math.cos(pt), 0, -math.sin(pt)], [0, 1, 0],
+                           [math.sin(pt), 0, math.cos(pt)]])
+            d = rz @ ry @ np.array([1.0, 0.0, 0.0])
+            t = 0.0
+            for _ in range(steps):
+                q = (eye + d * t - mins) / cell
+                i = np.clip(np.floor(q).astype(int), 0, [nx - 1, ny - 1, nz - 1])
+                s = float(grid[i[2], i[1], i[0]])
+                if not (s > eps and t < rng):
+                    break
+                t += max(0.9 * s, mstep)
+            t = min(t, rng)
+            img[r, c] = min(t, near) / near + 0.25 * (1.0 - math.exp(-max(t - near, 0.0) / 2500.0))
+    return img
+
+
+def test_oracle_agrees_with_an_independent_float64_march():
+    """The oracle (fp32, the reference's operation order) against a float64
+    re-march on small images of a real scene: a wrong axis, sign, index or
+    step term would move most rays; fp32 against fp64 rounding moves only
+    the rare ray whose sample sits on a voxel boundary."""
+    from surfgym import synth
+    w = synth.WORKLOADS["small_ramps"]
+    sc = w.scene()
+    ps = w.poses(sc, 6)
+    W, H = 16, 8
+    enc, _ = oracle.render(sc.sdf, sc.mins, sc.cell, ps.origin, ps.yaw, ps.pitch, ps.ducked,
+                           width=W, height=H, range_units=w.range_units,
+                           near_range=w.near_range, hit_eps=w.hit_eps, max_steps=w.max_steps)
+    mins = np.asarray(sc.mins, np.float64)
+    close = total = 0
+    for n in range(len(ps)):
+        eye = np.asarray(ps.origin[n], np.float64) + [0, 0, 12.0 if ps.ducked[n] else 17.0]
+        ref = _remarch_f64(np.asarray(sc.sdf, np.float64), mins, sc.cell, eye, float(ps.yaw[n]),
+                           float(ps.pitch[n]), W, H, w.range_units, w.near_range, w.hit_eps,
+                           0.3 * sc.cell, w.max_steps)
+        close += int((np.abs(enc[n] - ref) <= 1e-3).sum())
+        total += ref.size
+    assert close / total >= 0.99, f"{close}/{total} rays agree"
+
+
 # ------------------------------------------------------------------ SDF bake --
 def test_bake_matches_brute_force_on_tiny_grids():
     """oracle.edt.bake is the reference's scipy call (vision.py:428-432); an
