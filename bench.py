@@ -323,8 +323,8 @@ def main(argv=None):
     ap.add_argument("--schedule", default="tiles", choices=["persistent", "tiles", "slots"])
     ap.add_argument("--refill", type=int, default=16, help="free lanes that trigger a refill")
     ap.add_argument("--rpl", type=int, default=None,
-                    help="rays per lane: tiles 1-2, slots 1-4 (default: the library's choice, "
-                         "2 for cache-resident grids, 1 above 192 MiB)")
+                    help="rays per lane: tiles 1-2, slots 1-4 (default: the library's choice "
+                         "per render: 1 above 192 MiB and below 65536 tiles, else 2)")
     ap.add_argument("--tile-order", default="lookahead", choices=["lookahead", "launch"],
                     help="order the tiles schedule takes tiles in (library default: lookahead)")
     ap.add_argument("--cpu-envs", type=int, default=2048,
