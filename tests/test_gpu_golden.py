@@ -44,3 +44,13 @@ def test_gpu_matches_the_golden_fixture(dev):
                                       **kw)
     assert np.array_equal(lid_h.render(*poses, taps=taps).cpu().numpy(), g["f16"])
     assert np.array_equal(taps.cpu().numpy(), g["f16_loads"])
+    # the same at two rays per lane (these 3 envs render at one by default;
+    # fp16 bricks then also pack slots)
+    for lid_x in (lid, lid_m, lid_p, lid_h):
+        lid_x.set_schedule("tiles", rays_per_lane=2)
+    assert np.array_equal(lid.render(*poses, taps=taps).cpu().numpy(), g["enc"])
+    assert np.array_equal(taps.cpu().numpy(), g["loads"])
+    assert np.array_equal(lid_m.render(*poses).cpu().numpy(), g["surf"])
+    assert np.array_equal(lid_p.render(*poses).cpu().numpy(), g["pinhole"])
+    assert np.array_equal(lid_h.render(*poses, taps=taps).cpu().numpy(), g["f16"])
+    assert np.array_equal(taps.cpu().numpy(), g["f16_loads"])

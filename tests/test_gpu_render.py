@@ -516,9 +516,10 @@ def test_tile_order_with_pinhole_ragged_and_surf_mask(dev):
     snz = np.random.default_rng(3).integers(0, 128, sc.sdf.shape).astype(np.int8)
     # 37x19 and 8x8 over 5 envs give odd tile counts (75 and 5): the last run
     # of the order holds one tile, and every tile must still be marched once
-    for kw in (dict(pinhole=True), dict(width=37, height=19), dict(width=8, height=8),
+    for kw in (dict(pinhole=True, rays_per_lane=2), dict(width=37, height=19, rays_per_lane=2),
+               dict(width=8, height=8, rays_per_lane=2),
                dict(width=37, height=19, rays_per_lane=1), dict(width=8, height=8, rays_per_lane=1),
-               dict(surf_nz=snz)):
+               dict(surf_nz=snz, rays_per_lane=2), dict(surf_nz=snz)):
         kw.setdefault("width", w.width)
         kw.setdefault("height", w.height)
         lid = vision.GpuLidar.from_grid(sc.sdf, sc.mins, sc.cell, range_units=w.range_units,

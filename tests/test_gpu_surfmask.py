@@ -84,19 +84,22 @@ def test_flat_image_is_channel_fastest(dev):
     assert torch.equal(obs[:, 15:], flat) and torch.all(obs[:, :15] == -3.0)
 
 
-@pytest.mark.parametrize("layout,out_dtype", [("brick4", torch.float32), ("linear", torch.float32),
-                                              ("brick4", torch.bfloat16)])
-def test_both_channels_match_the_oracle(dev, layout, out_dtype):
+@pytest.mark.parametrize("layout,out_dtype,rpl", [("brick4", torch.float32, None),
+                                                  ("linear", torch.float32, None),
+                                                  ("brick4", torch.bfloat16, None),
+                                                  ("brick4", torch.float32, 2)])
+def test_both_channels_match_the_oracle(dev, layout, out_dtype, rpl):
     w = synth.WORKLOADS["small_ramps"]
     sc = w.scene()
     ps = w.poses(sc)
     rng = np.random.default_rng(7)
     snz = rng.integers(0, 128, sc.sdf.shape).astype(np.int8)
-    print(f"case surf-mask parity layout={layout} out={out_dtype}", flush=True)
+    print(f"case surf-mask parity layout={layout} out={out_dtype} rpl={rpl}", flush=True)
     lid = vision.GpuLidar.from_grid(sc.sdf, sc.mins, sc.cell, surf_nz=snz,
                                     range_units=w.range_units, near_range=w.near_range,
                                     max_steps=w.max_steps, hit_eps=w.hit_eps,
-                                    grid_dtype=torch.float32, layout=layout, device=dev)
+                                    grid_dtype=torch.float32, layout=layout, device=dev,
+                                    rays_per_lane=rpl)
     n = len(ps)
     out = torch.empty(n, w.height, w.width, 2, dtype=out_dtype, device=dev)
     taps = torch.empty(n, w.height, w.width, dtype=torch.int32, device=dev)
