@@ -552,16 +552,17 @@ def test_persistent_relaunches_reuse_their_counters(dev):
         assert torch.equal(out, full[:n]), n
 
 
-@pytest.mark.parametrize("sort,grid_dtype", [(False, torch.float32), (True, torch.float32),
-                                             (True, torch.float16)])
-def test_render_inside_a_captured_graph(dev, sort, grid_dtype):
+@pytest.mark.parametrize("sort,grid_dtype,rpl", [(False, torch.float32, None),
+                                                 (True, torch.float32, 2),
+                                                 (True, torch.float16, 2)])
+def test_render_inside_a_captured_graph(dev, sort, grid_dtype, rpl):
     """A hipGraph of one render replays correctly, again and again, with
     eager work between replays (the kernels clear their own counters: the
     persistent schedule's tile counters, the tile order's bucket counts)."""
     w, sc = _scene("small_ramps")
     ps = w.poses(sc)
-    _say(f"case graph capture sort={sort} grid={grid_dtype}")
-    lid = _lidar(dev, w, sc, grid_dtype=grid_dtype)
+    _say(f"case graph capture sort={sort} grid={grid_dtype} rpl={rpl}")
+    lid = _lidar(dev, w, sc, grid_dtype=grid_dtype, rays_per_lane=rpl)
     if sort:
         lid.set_tile_order("lookahead", min_tiles=0)   # sort even this small batch
     origin = torch.as_tensor(ps.origin, device=dev)
