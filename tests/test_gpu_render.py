@@ -748,3 +748,27 @@ def test_bench_configurations_are_bit_exact_at_full_size(dev, name):
     exact = float((got == want_t).float().mean())
     _say(f"{name}: {got.numel()} rays, exact {exact:.6f}")
     assert torch.equal(got, want_t)
+
+
+@pytest.mark.parametrize("variant", ["pinhole", "surf_mask"])
+def test_variants_are_bit_exact_at_the_headline_size(dev, variant):
+    """The two render variants at 2048 envs x 128x64 on ramp_field (sorted
+    tiles, two rays per lane): every output equals the oracle's."""
+    w, sc = _scene("ramp_field")
+    ps = w.poses(sc)
+    _say(f"case full-size variant {variant} envs={len(ps)}")
+    kw, okw = {}, {}
+    if variant == "pinhole":
+        kw["pinhole"] = okw["pinhole"] = True
+    else:
+        snz = np.random.default_rng(11).integers(0, 128, sc.sdf.shape).astype(np.int8)
+        kw["surf_nz"] = okw["surf_nz"] = snz
+    lid = vision.GpuLidar.from_grid(sc.sdf, sc.mins, sc.cell, width=w.width, height=w.height,
+                                    range_units=w.range_units, near_range=w.near_range,
+                                    max_steps=w.max_steps, hit_eps=w.hit_eps,
+                                    grid_dtype=torch.float32, device=dev, **kw)
+    assert lid.effective_rays_per_lane(len(ps)) == 2
+    got = _gpu_render(lid, ps, dev).cpu().numpy()
+    want, _ = _oracle(w, sc, ps, **okw)
+    assert got.shape == want.shape
+    assert np.array_equal(got, want)
