@@ -772,3 +772,21 @@ def test_variants_are_bit_exact_at_the_headline_size(dev, variant):
     want, _ = _oracle(w, sc, ps, **okw)
     assert got.shape == want.shape
     assert np.array_equal(got, want)
+
+
+def test_a_batch_of_16384_envs_equals_its_halves(dev):
+    """Batch independence beyond the bench sizes: 16384 envs x 128x64
+    (268 M rays, 262144 sorted units, 1 GiB of output) render exactly as
+    their two halves do apart."""
+    w, sc = _scene("ramp_field")
+    ps = w.poses(sc, 16384)
+    _say("case 16384 envs")
+    lid = _lidar(dev, w, sc)
+    args = [torch.as_tensor(v, device=dev) for v in (ps.origin, ps.yaw, ps.pitch, ps.ducked)]
+    full = lid.render(*args)
+    h = 8192
+    lo = lid.render(*[a[:h] for a in args])
+    assert torch.equal(full[:h], lo)
+    del lo
+    hi = lid.render(*[a[h:] for a in args])
+    assert torch.equal(full[h:], hi)
