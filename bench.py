@@ -111,17 +111,51 @@ class HipEvents:
         self.ev = []
 
 
-def profiled_traffic(key):
-    """L2-miss traffic per launch recorded for this configuration by the
-    FETCH_SIZE / WRITE_SIZE counter runs summarised under profiles/ (a line
-    ``traffic_bytes_per_launch[<key>] = <bytes>``), or None."""
+SDFR_SOURCE = ROOT / "rl_cs1.6_surf_amd" / "csrc" / "sdfr.hip"
+
+
+def sdfr_source_sha256():
+    """Hash of the render kernels' source: the profiles under profiles/
+    record it, so a figure measured on another version of the kernels is
+    recognised as stale."""
+    import hashlib
+    return hashlib.sha256(SDFR_SOURCE.read_bytes()).hexdigest()
+
+
+def profile_records():
+    """Per-workload records of the rocprofv3 summaries under profiles/: the
+    lines ``traffic_bytes_per_launch[<key>] = <bytes>`` and
+    ``limiter[<workload>] = <json>``, each with the file it came from and
+    the file's ``sdfr_hip_sha256 = <hex>`` (the kernels it was measured on)."""
     import re
+    traffic, limiter = {}, {}
     for f in sorted((ROOT / "profiles").glob("*.md")):
-        for line in f.read_text().splitlines():
-            m = re.match(r"traffic_bytes_per_launch\[(.+?)\] = (\d+)", line.strip())
-            if m and m.group(1) == key:
-                return int(m.group(2))
-    return None
+        text = f.read_text()
+        m = re.search(r"^sdfr_hip_sha256 = ([0-9a-f]{64})\s*$", text, re.M)
+        src = {"profile": f"profiles/{f.name}", "sdfr_hip_sha256": m.group(1) if m else None}
+        for line in text.splitlines():
+            line = line.strip()
+            t = re.match(r"traffic_bytes_per_launch\[(.+?)\] = (\d+)$", line)
+            if t:
+                traffic[t.group(1)] = dict(src, bytes=int(t.group(2)))
+            lm = re.match(r"limiter\[(.+?)\] = (\{.*\})$", line)
+            if lm:
+                limiter[lm.group(1)] = dict(src, **json.loads(lm.group(2)))
+    return traffic, limiter
+
+
+def profiled(key, table, field=None):
+    """The record for `key`, marked current or stale against the kernels'
+    source as it is now (a stale figure is reported as None)."""
+    rec = table.get(key)
+    if rec is None:
+        return None, None
+    current = rec.get("sdfr_hip_sha256") == sdfr_source_sha256()
+    src = {"profile": rec["profile"], "sdfr_hip_sha256": rec.get("sdfr_hip_sha256"),
+           "current": current}
+    value = (rec[field] if field else {k: v for k, v in rec.items()
+                                      if k not in ("profile", "sdfr_hip_sha256")})
+    return (value if current else None), src
 
 
 def copy_bandwidth(dev, n_bytes=2_000_000_000, iters=10):
@@ -313,6 +347,139 @@ def bench_goal(args, dev):
     print(json.dumps(res), flush=True)
 
 
+def alg_bytes_per_load(store):
+    """Grid bytes one sample reads: the voxel (4 B fp32, 2 B fp16), or for
+    r16 bricks the 2 B code and its brick's 8 B header (base, scale)."""
+    return {"f32": 4, "f16": 2, "r16": 10}[store]
+
+
+def measure_render(w, args, dev, *, graph, steps, warmup, out_shape=None, sc=None):
+    """One workload: scene and poses, a lidar with the library defaults (or
+    the command line's overrides), a census render (untimed) for the
+    algorithmic bytes, then `warmup` untimed and `steps` timed renders back
+    to back between two HIP events (eager, or replays of a captured graph),
+    and a second pass of `steps` renders with events around each render and
+    around each march kernel. Returns the figures as a dict."""
+    import torch
+    from surfgym import vision
+    t0 = time.perf_counter()
+    if sc is None:
+        sc = w.scene()
+    ps = w.poses(sc)
+    _log(f"[bench] {w.name}: grid {sc.nz}x{sc.ny}x{sc.nx} baked, {len(ps)} poses "
+         f"({time.perf_counter() - t0:.1f} s)")
+    gdt = {"f32": torch.float32, "f16": torch.float16, "r16": "r16"}[w.store]
+    odt = torch.bfloat16 if w.out_dtype == "bf16" else torch.float32
+    lid = vision.GpuLidar.from_grid(sc.sdf, sc.mins, sc.cell, width=w.width, height=w.height,
+                                    range_units=w.range_units, near_range=w.near_range,
+                                    max_steps=w.max_steps, hit_eps=w.hit_eps, grid_dtype=gdt,
+                                    layout=args.layout, schedule=args.schedule,
+                                    refill_lanes=args.refill, rays_per_lane=args.rpl,
+                                    tile_order=args.tile_order, device=dev)
+    origin = torch.as_tensor(ps.origin, device=dev)
+    yaw = torch.as_tensor(ps.yaw, device=dev)
+    pitch = torch.as_tensor(ps.pitch, device=dev)
+    duck = torch.as_tensor(ps.ducked, device=dev)
+    n = len(ps)
+    out = torch.empty(out_shape(n) if out_shape else (n, w.height, w.width), dtype=odt,
+                      device=dev)
+
+    # census (untimed): grid loads per ray -> algorithmic bytes
+    taps = torch.empty(n, w.height, w.width, dtype=torch.int32, device=dev)
+    lid.render(origin, yaw, pitch, duck, out=out, taps=taps)
+    torch.cuda.synchronize()
+    loads = int(taps.sum(dtype=torch.int64).item())
+    max_taps = int(taps.max().item())
+    del taps
+    rays = n * w.width * w.height
+    out_b = 2 if w.out_dtype == "bf16" else 4
+    alg_bytes = loads * alg_bytes_per_load(w.store) + rays * out_b + n * 24
+    _log(f"[bench] census: {loads} loads, mean {loads / rays:.2f}/ray, max {max_taps}")
+
+    step = lambda: lid.render(origin, yaw, pitch, duck, out=out)   # noqa: E731
+    g = None
+    if graph:
+        # the rollout step's render as a captured graph (capture on a side
+        # stream after an eager warm-up render, then replay on the current one)
+        side = torch.cuda.Stream(device=dev)
+        side.wait_stream(torch.cuda.current_stream(dev))
+        with torch.cuda.stream(side):
+            lid.render(origin, yaw, pitch, duck, out=out)
+        torch.cuda.current_stream(dev).wait_stream(side)
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            lid.render(origin, yaw, pitch, duck, out=out)
+        step = g.replay
+    stream = torch.cuda.current_stream(dev)
+    for _ in range(warmup):
+        step()
+    # events 0 and 1 bracket the timed region: K renders back to back, with
+    # nothing else on the stream (event markers between renders would add
+    # their own gaps). A second pass of K renders, outside the timed
+    # region, records 2 + 4k / 3 + 4k around render k and has the library
+    # record 4 + 4k / 5 + 4k around its march kernel; graph replays, whose
+    # launches were captured before, take those from K eager renders of the
+    # same batch.
+    ev = HipEvents(2 + 4 * steps)
+    sp = stream.cuda_stream
+    torch.cuda.synchronize()
+    t_start = time.perf_counter()
+    ev.record(0, sp)
+    for _ in range(steps):
+        step()
+    ev.record(1, sp)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t_start
+    for k in range(steps):
+        ev.record(2 + 4 * k, sp)
+        step()
+        ev.record(3 + 4 * k, sp)
+    for k in range(steps):
+        lid.set_march_events(ev.ev[4 + 4 * k].value, ev.ev[5 + 4 * k].value)
+        lid.render(origin, yaw, pitch, duck, out=out)
+    torch.cuda.synchronize()
+    lid.set_march_events(None, None)
+    total_ms = ev.ms(0, 1)
+    launch_ms = [ev.ms(2 + 4 * k, 3 + 4 * k) for k in range(steps)]
+    march_ms = [ev.ms(4 + 4 * k, 5 + 4 * k) for k in range(steps)]
+    ev.close()
+    ms_per_step = total_ms / steps
+    kernel_ms = sum(march_ms) / len(march_ms)
+    _log(f"[bench] {w.name}: {steps} steps: {ms_per_step:.4f} ms/step (events), wall {wall:.3f} s, "
+         f"launch median {statistics.median(launch_ms):.4f} ms; march kernel avg "
+         f"{kernel_ms * 1e3:.1f} us, median {statistics.median(march_ms) * 1e3:.1f} us")
+    res = {"workload": w.name, "envs": n, "rays": rays, "sc": sc, "lid": lid,
+           "grid": f"{sc.nx}x{sc.ny}x{sc.nz} {w.store} @{sc.cell:g}u", "store": w.store,
+           "out": w.out_dtype, "out_shape": list(out.shape), "graph": bool(graph),
+           "ms_per_step": ms_per_step, "launch_ms_median": statistics.median(launch_ms),
+           "march_kernel_ms_avg": kernel_ms, "loads": loads, "alg_bytes": alg_bytes,
+           "rpl": lid.effective_rays_per_lane(n)}
+    return res
+
+
+def config_summary(r):
+    """A workload's figures for the `configs` object of the JSON line."""
+    achieved = r["alg_bytes"] / (r["march_kernel_ms_avg"] * 1e-3) / 1e9
+    return {"envs": r["envs"], "rays": r["rays"], "grid": r["grid"], "out": r["out"],
+            "out_shape": r["out_shape"], "graph": r["graph"],
+            "ms_per_batch": round(r["ms_per_step"], 5),
+            "g_rays_per_s": round(r["rays"] / (r["ms_per_step"] * 1e-3) / 1e9, 4),
+            "march_kernel_ms_avg": round(r["march_kernel_ms_avg"], 5),
+            "grid_loads_per_ray": round(r["loads"] / r["rays"], 4),
+            "alg_bytes_per_launch": r["alg_bytes"],
+            "alg_frac_of_hbm_peak": round(achieved / HBM_PEAK_GBS, 5),
+            "rays_per_lane": r["rpl"]}
+
+
+# The other workloads of the metric, timed in the same run (GPU legs only):
+# (workload, captured graph, output shape)
+OTHER_CONFIGS = (("small_ramps", False, None),
+                 ("winding_track", False, None),
+                 ("sparse_grazing", False, None),
+                 ("ramp_field_r16_bf16", True, lambda n: (n, 1, 64, 128)))
+
+
 def main(argv=None):
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -320,17 +487,21 @@ def main(argv=None):
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--workload", default="ramp_field")
     ap.add_argument("--layout", default="brick4", choices=["brick4", "linear"])
-    ap.add_argument("--schedule", default="tiles", choices=["persistent", "tiles", "slots"])
+    ap.add_argument("--schedule", default="tiles", choices=["persistent", "tiles"])
     ap.add_argument("--refill", type=int, default=16, help="free lanes that trigger a refill")
     ap.add_argument("--rpl", type=int, default=None,
-                    help="rays per lane: tiles 1-2, slots 1-4 (default: the library's choice "
-                         "per render: 1 above 192 MiB and below 65536 tiles, else 2)")
+                    help="rays per lane, 1 or 2 (default: the library's choice per render: "
+                         "1 above 192 MiB and below 65536 tiles, else 2)")
     ap.add_argument("--tile-order", default="lookahead", choices=["lookahead", "launch"],
                     help="order the tiles schedule takes tiles in (library default: lookahead)")
     ap.add_argument("--cpu-envs", type=int, default=2048,
                     help="envs of the workload the CPU baseline renders (default: all of ramp_field)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-copy", action="store_true", help="skip the copy-bandwidth probe")
+    ap.add_argument("--no-configs", action="store_true",
+                    help="time the one workload only (not the other configurations)")
+    ap.add_argument("--config-steps", type=int, default=20,
+                    help="timed renders per other configuration")
     ap.add_argument("--bake", action="store_true",
                     help="time the SDF bake (GPU distance transform of the workload's "
                          "occupancy) against the reference's scipy bake instead")
@@ -347,9 +518,8 @@ def main(argv=None):
         sys.exit("bench.py measures one GPU: the render is per-env data parallel with no "
                  "exchange, and this build runs on a single MI355X (use --gpus 1)")
 
-    import numpy as np
     import torch
-    from surfgym import synth, vision
+    from surfgym import synth
 
     dev = torch.device("cuda:0")
     if args.goal:
@@ -357,104 +527,20 @@ def main(argv=None):
     w = synth.WORKLOADS[args.workload]
     if args.bake:
         return bench_bake(args, w, dev)
-    t0 = time.perf_counter()
-    sc = w.scene()
-    ps = w.poses(sc)
-    _log(f"[bench] {w.name}: grid {sc.nz}x{sc.ny}x{sc.nx} baked, {len(ps)} poses "
-         f"({time.perf_counter() - t0:.1f} s)")
-    gdt = torch.float16 if w.store == "f16" else torch.float32
-    odt = torch.bfloat16 if w.out_dtype == "bf16" else torch.float32
-    lid = vision.GpuLidar.from_grid(sc.sdf, sc.mins, sc.cell, width=w.width, height=w.height,
-                                    range_units=w.range_units, near_range=w.near_range,
-                                    max_steps=w.max_steps, hit_eps=w.hit_eps, grid_dtype=gdt,
-                                    layout=args.layout, schedule=args.schedule,
-                                    refill_lanes=args.refill, rays_per_lane=args.rpl,
-                                    tile_order=args.tile_order, device=dev)
-    origin = torch.as_tensor(ps.origin, device=dev)
-    yaw = torch.as_tensor(ps.yaw, device=dev)
-    pitch = torch.as_tensor(ps.pitch, device=dev)
-    duck = torch.as_tensor(ps.ducked, device=dev)
-    n = len(ps)
-    out = torch.empty(n, w.height, w.width, dtype=odt, device=dev)
-
-    # census (untimed): grid loads per ray -> algorithmic bytes
-    taps = torch.empty(n, w.height, w.width, dtype=torch.int32, device=dev)
-    lid.render(origin, yaw, pitch, duck, out=out, taps=taps)
-    torch.cuda.synchronize()
-    loads = int(taps.sum(dtype=torch.int64).item())
-    tap_stats = taps.float()
-    rays = n * w.width * w.height
-    vox_b = 2 if w.store == "f16" else 4
-    out_b = 2 if w.out_dtype == "bf16" else 4
-    alg_bytes = loads * vox_b + rays * out_b + n * 24
-    _log(f"[bench] census: {loads} loads, mean {loads / rays:.2f}/ray, "
-         f"max {int(tap_stats.max().item())}")
-    del taps, tap_stats
-
-    step = lambda: lid.render(origin, yaw, pitch, duck, out=out)   # noqa: E731
-    if args.graph:
-        # the rollout step's render as a captured graph (capture on a side
-        # stream after an eager warm-up render, then replay on the current one)
-        side = torch.cuda.Stream(device=dev)
-        side.wait_stream(torch.cuda.current_stream(dev))
-        with torch.cuda.stream(side):
-            lid.render(origin, yaw, pitch, duck, out=out)
-        torch.cuda.current_stream(dev).wait_stream(side)
-        torch.cuda.synchronize()
-        graph = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(graph):
-            lid.render(origin, yaw, pitch, duck, out=out)
-        step = graph.replay
-    stream = torch.cuda.current_stream(dev)
-    for _ in range(args.warmup):
-        step()
-    # events 0 and 1 bracket the timed region: K renders back to back, with
-    # nothing else on the stream (event markers between renders would add
-    # their own gaps). A second pass of K renders, outside the timed
-    # region, records 2 + 4k / 3 + 4k around render k and has the library
-    # record 4 + 4k / 5 + 4k around its march kernel (not for graph replays,
-    # whose launches were captured before): the per-render and per-kernel
-    # durations behind the medians and the roofline.
-    ev = HipEvents(2 + 4 * args.steps)
-    sp = stream.cuda_stream
-    march_events = not args.graph
-    torch.cuda.synchronize()
-    t_start = time.perf_counter()
-    ev.record(0, sp)
-    for k in range(args.steps):
-        step()
-    ev.record(1, sp)
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - t_start
-    for k in range(args.steps):
-        if march_events:
-            lid.set_march_events(ev.ev[4 + 4 * k].value, ev.ev[5 + 4 * k].value)
-        ev.record(2 + 4 * k, sp)
-        step()
-        ev.record(3 + 4 * k, sp)
-    torch.cuda.synchronize()
-    if march_events:
-        lid.set_march_events(None, None)
-    total_ms = ev.ms(0, 1)
-    launch_ms = [ev.ms(2 + 4 * k, 3 + 4 * k) for k in range(args.steps)]
-    march_ms = [ev.ms(4 + 4 * k, 5 + 4 * k) for k in range(args.steps)] if march_events else None
-    ev.close()
-    ms_per_step = total_ms / args.steps
-    avg_launch_ms = sum(launch_ms) / len(launch_ms)
-    med_launch_ms = statistics.median(launch_ms)
-    # the roofline's kernel is the march: its own average duration when the
-    # library timed it, else the whole render's
-    kernel_ms = sum(march_ms) / len(march_ms) if march_ms else avg_launch_ms
-    achieved = alg_bytes / (kernel_ms * 1e-3) / 1e9
-    _log(f"[bench] {args.steps} steps: {ms_per_step:.4f} ms/step (events), wall {wall:.3f} s, "
-         f"launch avg {avg_launch_ms:.4f} ms, median {med_launch_ms:.4f} ms"
-         + (f"; march kernel avg {kernel_ms * 1e3:.1f} us, median "
-            f"{statistics.median(march_ms) * 1e3:.1f} us" if march_ms else ""))
+    r = measure_render(w, args, dev, graph=args.graph, steps=args.steps, warmup=args.warmup)
+    sc, lid = r.pop("sc"), r.pop("lid")
+    n, rays = r["envs"], r["rays"]
+    ms_per_step, kernel_ms = r["ms_per_step"], r["march_kernel_ms_avg"]
+    achieved = r["alg_bytes"] / (kernel_ms * 1e-3) / 1e9
+    rpl = r["rpl"]
+    traffic_tab, limiter_tab = profile_records()
+    traffic, traffic_src = profiled(f"{w.name} {args.schedule} rpl={rpl} {args.layout} {w.store}"
+                                    f" order={lid.tile_order}", traffic_tab, "bytes")
+    limiter, limiter_src = profiled(w.name, limiter_tab)
+    del lid
+    torch.cuda.empty_cache()
 
     copy_gbs = None if args.no_copy else copy_bandwidth(dev)
-    rpl = lid.effective_rays_per_lane(n)
-    traffic = profiled_traffic(f"{w.name} {args.schedule} rpl={rpl} {args.layout} {w.store}"
-                               f" order={lid.tile_order}")
     if copy_gbs:
         _log(f"[bench] device copy {copy_gbs:.0f} GB/s")
     res = {
@@ -471,22 +557,39 @@ def main(argv=None):
         "dtype": "f32",
         "data": "synthetic",
         "config": {"workload": w.name, "envs": n, "image": f"{w.width}x{w.height}",
-                   "rays": rays, "grid": f"{sc.nx}x{sc.ny}x{sc.nz} {w.store} @{sc.cell:g}u",
+                   "rays": rays, "grid": r["grid"],
                    "layout": args.layout, "schedule": args.schedule, "refill_lanes": args.refill,
-                   "rays_per_lane": rpl, "tile_order": lid.tile_order,
+                   "rays_per_lane": rpl, "tile_order": args.tile_order,
                    "out": w.out_dtype, "max_steps": w.max_steps,
                    "hit_eps": w.hit_eps, "range": round(w.range_units, 3),
-                   "near": round(w.near_range, 3), "grid_loads_per_ray": round(loads / rays, 4),
+                   "near": round(w.near_range, 3),
+                   "grid_loads_per_ray": round(r["loads"] / rays, 4),
                    "graph": bool(args.graph),
-                   "launch_ms_median": round(med_launch_ms, 5),
-                   "march_kernel_ms_avg": round(kernel_ms, 5) if march_ms else None},
+                   "launch_ms_median": round(r["launch_ms_median"], 5),
+                   "march_kernel_ms_avg": round(kernel_ms, 5)},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 5), "traffic": traffic,
-                     "alg_bytes_per_launch": alg_bytes,
+                     "traffic_source": traffic_src,
+                     "alg_bytes_per_launch": r["alg_bytes"],
                      "copy_gbs": round(copy_gbs, 1) if copy_gbs else None,
-                     "frac_of_copy": round(achieved / copy_gbs, 5) if copy_gbs else None},
+                     "frac_of_copy": round(achieved / copy_gbs, 5) if copy_gbs else None,
+                     "limiter": limiter, "limiter_source": limiter_src},
+        "configs": None,
         "cpu_baseline": None,
     }
+    if not args.no_configs:
+        configs = {}
+        for name, graph, shape in OTHER_CONFIGS:
+            if name == w.name:
+                continue
+            cw = synth.WORKLOADS[name]
+            cr = measure_render(cw, args, dev, graph=graph, steps=args.config_steps,
+                                warmup=min(args.warmup, 5), out_shape=shape)
+            cr.pop("lid")
+            cr.pop("sc")
+            configs[name] = config_summary(cr)
+            torch.cuda.empty_cache()
+        res["configs"] = configs
     if not args.no_cpu:
         envs = min(args.cpu_envs, n)
         _log(f"[bench] cpu baseline on {envs} envs ...")

@@ -34,7 +34,7 @@ extern "C" {
 
 /* Bumped on every struct or semantic change; the binding refuses a library
  * reporting another value. */
-#define SDFR_ABI_VERSION 11
+#define SDFR_ABI_VERSION 12
 
 /* Element types of caller arrays. */
 enum {
@@ -45,7 +45,11 @@ enum {
     SDFR_I64 = 4,
     SDFR_U8 = 5,   /* also torch.bool */
     SDFR_F64 = 6,
-    SDFR_U16 = 7   /* goal-field grids */
+    SDFR_U16 = 7,  /* goal-field grids */
+    SDFR_R16 = 8   /* grid store only: 4x4x4 bricks of uint16 codes, each brick with an fp32
+                      base (its smallest value) and an fp32 power-of-two scale; a voxel reads
+                      f32(base + code*scale), within scale/2 (plus one fp32 rounding) of the
+                      source value; scale <= 2^-9 u for a distance field at 16 u cells */
 };
 
 /* Device layout of the handle's private copy of the grid. */
@@ -63,8 +67,7 @@ enum {
 /* Work schedules of sdfr_render (both give identical results). */
 enum {
     SDFR_SCHED_PERSISTENT = 0, /* persistent waves refilling ended rays' lanes */
-    SDFR_SCHED_TILES = 1,      /* default: launch-scheduled waves of 8x8 pixel tiles */
-    SDFR_SCHED_SLOTS = 2       /* persistent waves of R tile slots, a drained slot takes a new tile */
+    SDFR_SCHED_TILES = 1       /* default: launch-scheduled waves of 8x8 pixel tiles */
 };
 
 /* The order in which the tiles schedule takes 8x8 pixel tiles. */
@@ -137,10 +140,10 @@ SDFR_API int32_t sdfr_abi_version(void);
 /* Builds the handle's device copy of a grid. `src` holds nz*ny*nx values of
  * `src_dtype` (SDFR_F32 or SDFR_F16) in [nz][ny][nx] order; src_on_device
  * says whether it is a device pointer (a torch tensor) or host memory.
- * `store_dtype` (SDFR_F32 or SDFR_F16; the reference stores f16,
- * vision.py:476-477, rounding to nearest even) and `layout` (SDFR_LAYOUT_*)
- * pick the device copy. Replaces the grid upload of GpuLidar.__init__
- * (vision.py:473-480). The copy is complete when the stream reaches it;
+ * `store_dtype` (SDFR_F32; SDFR_F16, as the reference stores it,
+ * vision.py:476-477, rounding to nearest even; or SDFR_R16, brick4 layout
+ * only) and `layout` (SDFR_LAYOUT_*) pick the device copy. Replaces the
+ * grid upload of GpuLidar.__init__ (vision.py:473-480). The copy is complete when the stream reaches it;
  * the source may be freed after that. NULL + message in err on failure. */
 SDFR_API SdfrGrid* sdfr_grid_create(const SdfrGridDesc* desc, const void* src,
                                     int32_t src_dtype, int32_t src_on_device,
@@ -160,10 +163,10 @@ SDFR_API int32_t sdfr_grid_attach_surfnz(SdfrGrid* grid, const void* src, int32_
 /* Chooses how sdfr_render schedules rays on this handle: `schedule` is an
  * SDFR_SCHED_* value (default SDFR_SCHED_TILES); `refill_lanes` (1..64,
  * default 16) is the number of free lanes at which a persistent wave takes
- * new rays; `rays_per_lane` is how many tiles a wave marches at once: 1 or
- * 2 for the tiles schedule, 1..4 slots for the slots schedule, or 0 (the
- * default) to let each render choose: 1 for grids above 192 MiB and for
- * renders of fewer than 65536 tiles (512 envs of 128x64), else 2.
+ * new rays; `rays_per_lane` is how many tiles a wave of the tiles schedule
+ * marches at once: 1 or 2, or 0 (the default) to let each render choose: 1
+ * for grids above 192 MiB and for renders of fewer than 65536 tiles (512
+ * envs of 128x64), else 2.
  * Surf-mask renders always use the tiles schedule. Results do not depend
  * on any of them. Synchronous; 0 or < 0. No reference counterpart: the
  * Triton launch has one fixed shape (vision.py:48-54; tools/proto_march.py
@@ -171,9 +174,9 @@ SDFR_API int32_t sdfr_grid_attach_surfnz(SdfrGrid* grid, const void* src, int32_
 SDFR_API int32_t sdfr_grid_set_schedule(SdfrGrid* grid, int32_t schedule, int32_t refill_lanes,
                                         int32_t rays_per_lane);
 
-/* The rays per lane (tiles schedule) or slots per wave (slots schedule) a
- * render of `n_envs` images of `cam` would run with on this handle; < 0 on
- * bad arguments. No reference counterpart. */
+/* The rays per lane a render of `n_envs` images of `cam` would run with on
+ * this handle (tiles schedule and surf-mask renders); < 0 on bad arguments.
+ * No reference counterpart. */
 SDFR_API int32_t sdfr_render_rays_per_lane(const SdfrGrid* grid, const SdfrCam* cam,
                                            int32_t n_envs);
 
@@ -194,7 +197,8 @@ SDFR_API int32_t sdfr_grid_set_tile_order(SdfrGrid* grid, int32_t order, int64_t
  * events must stay valid while set; nulls clear them. Synchronous; 0 or < 0. */
 SDFR_API int32_t sdfr_grid_set_march_events(SdfrGrid* grid, void* start, void* stop);
 
-/* Bytes of device memory the handle owns (the re-laid-out grid). */
+/* Bytes of device memory the handle's grid copy occupies (r16: codes and
+ * brick headers). */
 SDFR_API int64_t sdfr_grid_bytes(const SdfrGrid* grid);
 
 /* Device bytes of the workspace sdfr_render needs for n_envs envs of this
@@ -216,6 +220,14 @@ SDFR_API int64_t sdfr_workspace_bytes(const SdfrCam* cam, int32_t n_envs);
 SDFR_API int32_t sdfr_render(const SdfrGrid* grid, const SdfrCam* cam,
                              const SdfrPoses* poses, const SdfrImage* image,
                              void* workspace, int64_t workspace_size, void* stream);
+
+/* Reads the handle's grid copy back as nz*ny*nx fp32 values in [nz][ny][nx]
+ * order: exactly the values the march samples (fp16 widened, r16 decoded).
+ * The reference's kernel samples its device tensor GpuLidar.sdf_flat
+ * (vision.py:476-480), which its tests read (tests/python/
+ * test_lidar_march.py:130-138); this is the same view of this library's
+ * private copy. `out`: device memory. Asynchronous on `stream`; 0 or < 0. */
+SDFR_API int32_t sdfr_grid_read(const SdfrGrid* grid, float* out, void* stream);
 
 /* Writes the unit direction of every ray, dirs[n][r][c][0..2] (dense f32),
  * with the same code the march uses to cast it; origin and ducked are not

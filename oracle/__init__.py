@@ -86,15 +86,64 @@ def _ptr(a: np.ndarray):
     return a.ctypes.data_as(ctypes.c_void_p)
 
 
+def r16_encode(grid: np.ndarray):
+    """The r16 brick store of a [nz,ny,nx] grid: (codes uint16 [bz,by,bx,64],
+    base float32 [bz,by,bx], exponent int [bz,by,bx]).
+
+    Per 4x4x4 brick of voxels (inner order x fastest, then y, then z; the
+    brick grid padded up to whole bricks): base = the smallest value of the
+    brick's voxels inside the grid; exponent e = the smallest integer >= -100
+    with (max - base) <= 65535 * 2^e, at most 100 (for max > base, e is
+    ilogb(max - base) - 15, plus one when that leaves the range above 65535
+    units); code = round-half-even((value - base) * 2^-e) in fp64, clamped to
+    [0, 65535] (NaN -> 0); padding voxels code 0. A storage format of this
+    renderer (no reference counterpart): it gives the reference's fp32 grid
+    values to within 2^(e-1) at two bytes per voxel.
+    """
+    g = np.ascontiguousarray(grid, dtype=np.float32)
+    nz, ny, nx = g.shape
+    bz, by, bx = (nz + 3) // 4, (ny + 3) // 4, (nx + 3) // 4
+    pad = np.full((bz * 4, by * 4, bx * 4), np.nan, np.float64)
+    pad[:nz, :ny, :nx] = g
+    # [bz, 4(z), by, 4(y), bx, 4(x)] -> [bz, by, bx, 4z, 4y, 4x] -> 64 per brick
+    b = pad.reshape(bz, 4, by, 4, bx, 4).transpose(0, 2, 4, 1, 3, 5).reshape(bz, by, bx, 64)
+    inside = ~np.isnan(b)
+    lo = np.where(inside, b, np.inf).min(axis=-1)
+    hi = np.where(inside, b, -np.inf).max(axis=-1)
+    rng = hi - lo                       # exact: differences of fp32 values in fp64
+    e = np.full(rng.shape, -100, np.int64)
+    pos = rng > 0
+    _, ex = np.frexp(rng[pos])          # rng = m * 2^ex, m in [0.5, 1): ilogb = ex - 1
+    ep = (ex - 1) - 15
+    ep = ep + (np.ldexp(rng[pos], -ep) > 65535.0)
+    e[pos] = np.clip(ep, -100, 100)
+    q = np.rint((b - lo[..., None]) * np.ldexp(1.0, -e)[..., None])
+    q = np.where(q >= 0.0, np.minimum(q, 65535.0), 0.0)   # NaN (padding) -> 0
+    return q.astype(np.uint16), lo.astype(np.float32), e
+
+
+def r16_decode(codes, base, exponent, shape) -> np.ndarray:
+    """Voxel values the renderer reads from an r16 store, [nz,ny,nx] f32:
+    f32(base + f32(code * 2^e)) (the product is exact in fp32)."""
+    nz, ny, nx = shape
+    bz, by, bx = base.shape
+    scale = np.ldexp(np.float32(1.0), exponent).astype(np.float32)
+    v = base[..., None] + codes.astype(np.float32) * scale[..., None]   # fp32 add, one rounding
+    v = v.astype(np.float32).reshape(bz, by, bx, 4, 4, 4).transpose(0, 3, 1, 4, 2, 5)
+    return np.ascontiguousarray(v.reshape(bz * 4, by * 4, bx * 4)[:nz, :ny, :nx])
+
+
 def as_stored(grid: np.ndarray, store: str) -> np.ndarray:
-    """The voxel values the renderer reads: f32 as given, or rounded to f16
+    """The voxel values the renderer reads: f32 as given; rounded to f16
     (round to nearest even, as torch's ``.to(torch.float16)``, vision.py:476)
-    and widened back."""
+    and widened back; or through the r16 brick store (:func:`r16_encode`)."""
     g = np.ascontiguousarray(grid, dtype=np.float32)
     if store in ("f16", "float16"):
         return g.astype(np.float16).astype(np.float32)
     if store in ("f32", "float32"):
         return g
+    if store == "r16":
+        return r16_decode(*r16_encode(g), g.shape)
     raise ValueError(f"unknown store dtype {store!r}")
 
 

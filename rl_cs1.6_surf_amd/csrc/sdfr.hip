@@ -30,7 +30,7 @@
 //      With the lookahead tile order the same launch also keys the tiles by
 //      where they look and counts them into buckets, and order_scatter
 //      writes the sorted list (see "tile order");
-//   2. the march, in one of three schedules with identical results:
+//   2. the march, in one of two schedules with identical results:
 //      - tiles (default): launch-scheduled two-wave workgroups, each wave
 //        marching RPL 8x8 pixel tiles at once, RPL rays per lane (1 or 2,
 //        chosen per render by render_rpl unless the caller fixes it);
@@ -39,12 +39,20 @@
 //        pulling 8x8 pixel tiles from per-XCD work counters. It keeps every
 //        lane busy but mixes rays of different depths in one gather, which
 //        costs more cache lines per gather than it saves in idle lanes on
-//        the scenes measured so far, so it is not the default;
-//      - slots: persistent waves of R tile slots (see march_slots).
+//        the scenes measured so far, so it is not the default.
 // Blocks are dealt to the 8 XCDs round-robin by the hardware; they are
 // numbered so that each XCD works on a contiguous run of envs (env order), or
 // on interleaved chunks of the sorted tile list (lookahead order), keeping
 // rays that share grid data in one L2.
+//
+// Grid storage (the handle's copy): fp32 or fp16 voxels, in 4x4x4 bricks or
+// the reference's linear order, or "r16" bricks: per 4x4x4 brick a header
+// (fp32 base = the brick's smallest value, fp32 scale = a power of two) and
+// 64 uint16 codes, the voxel value being f32(base + code*scale) with
+// |value - grid| <= scale/2 plus one fp32 rounding. Two bytes per voxel like
+// fp16, but the error is bounded by the brick's own value range (at most
+// ~3*sqrt(3)*cell for a distance field: 2^-9 u at 16 u cells) instead of by
+// the value's magnitude (fp16: 1 u at 1024-2048 u).
 
 #include <hip/hip_runtime.h>
 #include <hip/hip_fp16.h>
@@ -53,6 +61,8 @@
 #include <stdint.h>
 #include <stdio.h>
 #include <string.h>
+
+#include <type_traits>
 
 #include "../../include/sdfr.h"
 
@@ -130,11 +140,13 @@ __attribute__((format(printf, 2, 3))) int32_t fail(int32_t code, const char* fmt
 // ---------------------------------------------------------------- handle --
 struct SdfrGrid {
     SdfrGridDesc desc;
-    int32_t store_dtype;   // SDFR_F32 | SDFR_F16
+    int32_t store_dtype;   // SDFR_F32 | SDFR_F16 | SDFR_R16
     int32_t layout;        // SDFR_LAYOUT_*
     int32_t bx, by, bz;    // brick counts (BRICK4), else nx, ny, nz
     void* data;            // device copy
-    int64_t bytes;
+    int64_t bytes;         // all of it (r16: codes, padding and brick headers)
+    int64_t code_bytes;    // the voxel values (r16: the uint16 codes), from offset 0
+    int64_t hdr_off;       // r16: byte offset of the brick headers (float2 per brick), else 0
     uint32_t* counters;    // persistent schedule: tile claim counters + exit counter
     int32_t schedule;      // SDFR_SCHED_*
     int32_t refill_lanes;  // persistent schedule: refill when this many lanes are free
@@ -144,9 +156,12 @@ struct SdfrGrid {
     int device;
     int cus;               // compute units of the device
     int lds_per_cu;        // bytes of LDS per CU
+    int lds_per_block;     // largest LDS allocation of one workgroup
     int32_t tile_order;    // SDFR_ORDER_*: the order the tiles schedule takes tiles in
     int64_t order_min_tiles;  // ... applied to renders of at least this many tiles
     uint32_t* order_hist;  // tile-order bucket counts [kOrderBuckets]: zero between renders
+    mutable bool hist_dirty;  // a sorted render stopped after counting and before the march
+                              // that clears the counts: the next render clears them first
     void* march_events[2]; // caller's hipEvent_t pair around the march launch, or nulls
 };
 
@@ -183,15 +198,50 @@ __device__ __forceinline__ uint32_t axis_offset(int i, int nx, int ny, int layou
     return e << log_elem;
 }
 
+// Storage tag of r16 bricks (uint16 codes + per-brick float2 header).
+struct R16 {};
+
 template <typename GT>
-__device__ __forceinline__ float load_voxel(__amdgpu_buffer_rsrc_t rsrc, uint32_t off) {
-    if constexpr (sizeof(GT) == 2) {
-        const unsigned short h = __builtin_amdgcn_raw_buffer_load_b16(rsrc, off, 0, 0);
-        return __half2float(__ushort_as_half(h));
-    } else {
-        return __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rsrc, off, 0, 0));
-    }
+constexpr int kElemLog = std::is_same<GT, float>::value ? 2 : 1;   // log2 bytes per stored voxel
+
+// Slot packing of the tiles schedule (march_tiles) for 2-byte stores, where
+// a gather touches about half the lines of an fp32 one and vector issue is
+// the tighter bound.
+#ifndef SDFR_R16_PACK
+#define SDFR_R16_PACK 1
+#endif
+template <typename GT>
+constexpr bool kPackStore = std::is_same<GT, __half>::value ||
+                            (std::is_same<GT, R16>::value && SDFR_R16_PACK);
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, (int)bytes, kRsrcWord3);
 }
+
+// Reads the voxel at a byte offset of the copy (an offset from the axis
+// tables) as fp32. r16: code at `off`, header of its brick at (off / 128) * 8
+// (a brick's 64 codes are one 128-byte line); f32(base + code*scale) with the
+// product exact (16-bit code, power-of-two scale), so the fma rounds once,
+// as the add after an exact multiply does.
+template <typename GT>
+struct GridReader {
+    __amdgpu_buffer_rsrc_t codes, hdr;
+    __device__ GridReader(const void* data, uint32_t code_bytes, uint32_t hdr_off, uint32_t hdr_bytes)
+        : codes(make_rsrc(data, code_bytes)),
+          hdr(make_rsrc((const char*)data + hdr_off, hdr_bytes)) {}
+    __device__ __forceinline__ float operator()(uint32_t off) const {
+        if constexpr (std::is_same<GT, float>::value) {
+            return __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(codes, off, 0, 0));
+        } else if constexpr (std::is_same<GT, __half>::value) {
+            const unsigned short h = __builtin_amdgcn_raw_buffer_load_b16(codes, off, 0, 0);
+            return __half2float(__ushort_as_half(h));
+        } else {
+            const uint32_t q = __builtin_amdgcn_raw_buffer_load_b16(codes, off, 0, 0);
+            const auto bs = __builtin_amdgcn_raw_buffer_load_b64(hdr, (off >> 4) & ~7u, 0, 0);
+            return __builtin_fmaf((float)q, __uint_as_float(bs[1]), __uint_as_float(bs[0]));
+        }
+    }
+};
 
 // ------------------------------------------------------------- conversions --
 __device__ __forceinline__ uint16_t f32_to_bf16_rne(float f) {
@@ -248,11 +298,10 @@ __device__ __forceinline__ float2 sincos_f32(float x) {
 // --------------------------------------------------------------- the args --
 struct MarchArgs {
     const void* grid;
-    uint32_t grid_bytes;          // size of the device copy (the descriptor's range)
-    uint32_t dead_off;            // slots and persistent schedules: gather offset for ended
-                                  // rays, past the range (reads 0 without touching memory)
+    uint32_t code_bytes;          // bytes of voxel values from `grid` (the codes' descriptor range)
+    uint32_t hdr_off, hdr_bytes;  // r16: the brick headers' byte offset and size, else 0
     int nx, ny, nz, bx, by, layout;
-    int grid_f16;                 // the copy stores fp16 voxels (else fp32)
+    int store;                    // SDFR_F32 | SDFR_F16 | SDFR_R16
     float fnx1, fny1, fnz1;       // n-1 as float: the clamp bound
     float mnx, mny, mnz, inv_cell;
     float rng, near, hit_eps, min_step;
@@ -321,13 +370,13 @@ __device__ __forceinline__ float eye_sample(const MarchArgs& a, float ex, float 
     const int ix = (int)__builtin_amdgcn_fmed3f((ex - a.mnx) * a.inv_cell, 0.0f, a.fnx1);
     const int iy = (int)__builtin_amdgcn_fmed3f((ey - a.mny) * a.inv_cell, 0.0f, a.fny1);
     const int iz = (int)__builtin_amdgcn_fmed3f((ez - a.mnz) * a.inv_cell, 0.0f, a.fnz1);
-    const int lg = a.grid_f16 ? 1 : 2;
+    const int lg = a.store == SDFR_F32 ? 2 : 1;
     const uint32_t off = axis_offset(ix, a.nx, a.ny, a.layout, a.bx, a.by, lg) +
                          axis_offset(a.nx + iy, a.nx, a.ny, a.layout, a.bx, a.by, lg) +
                          axis_offset(a.nx + a.ny + iz, a.nx, a.ny, a.layout, a.bx, a.by, lg);
-    const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(
-        const_cast<void*>(a.grid), 0, (int)a.grid_bytes, kRsrcWord3);
-    return a.grid_f16 ? load_voxel<__half>(rsrc, off) : load_voxel<float>(rsrc, off);
+    if (a.store == SDFR_F32) return GridReader<float>(a.grid, a.code_bytes, 0, 0)(off);
+    if (a.store == SDFR_F16) return GridReader<__half>(a.grid, a.code_bytes, 0, 0)(off);
+    return GridReader<R16>(a.grid, a.code_bytes, a.hdr_off, a.hdr_bytes)(off);
 }
 
 // Eye height of env n: origin z + 12 ducked or 17 standing (vision.py:77-78).
@@ -405,7 +454,7 @@ __device__ __forceinline__ void store_enc(void* out, int64_t o, float enc) {
 // One march step of a live ray (vision.py:101-111). Returns whether the ray
 // is still alive; t advances only if it is.
 template <typename GT>
-__device__ __forceinline__ bool march_step(const MarchArgs& a, __amdgpu_buffer_rsrc_t rsrc,
+__device__ __forceinline__ bool march_step(const MarchArgs& a, const GridReader<GT>& rd,
                                            const uint32_t* __restrict__ tab, float ex, float ey,
                                            float ez, float dx, float dy, float dz, float& t) {
     const float px = ex + dx * t;
@@ -414,7 +463,7 @@ __device__ __forceinline__ bool march_step(const MarchArgs& a, __amdgpu_buffer_r
     const int ix = (int)__builtin_amdgcn_fmed3f((px - a.mnx) * a.inv_cell, 0.0f, a.fnx1);
     const int iy = (int)__builtin_amdgcn_fmed3f((py - a.mny) * a.inv_cell, 0.0f, a.fny1);
     const int iz = (int)__builtin_amdgcn_fmed3f((pz - a.mnz) * a.inv_cell, 0.0f, a.fnz1);
-    const float sd = load_voxel<GT>(rsrc, tab[ix] + tab[a.nx + iy] + tab[a.nx + a.ny + iz]);
+    const float sd = rd(tab[ix] + tab[a.nx + iy] + tab[a.nx + a.ny + iz]);
     const bool alive = (sd > a.hit_eps) && (t < a.rng);
     if (alive) t = t + fmaxf(sd * 0.9f, a.min_step);
     return alive;
@@ -422,7 +471,7 @@ __device__ __forceinline__ bool march_step(const MarchArgs& a, __amdgpu_buffer_r
 
 template <typename GT, int LAYOUT>
 __device__ __forceinline__ void fill_axis_tables(const MarchArgs& a, uint32_t* s_axis) {
-    constexpr int kLog = sizeof(GT) == 2 ? 1 : 2;
+    constexpr int kLog = kElemLog<GT>;
     const int ntab = a.nx + a.ny + a.nz;
     for (int i = threadIdx.x; i < ntab; i += blockDim.x)
         s_axis[i] = axis_offset(i, a.nx, a.ny, LAYOUT, a.bx, a.by, kLog);
@@ -636,7 +685,7 @@ __global__ __launch_bounds__(64 * kTileWaves) void march_tiles(MarchArgs a) {
     // many lines and vector issue is the tighter bound; on fp32 grids the
     // texture path binds and packing (rays of two tiles in one gather) costs
     // ~3% more L1 tag accesses than the instructions it saves.
-    constexpr bool kPack = RPL == 2 && !SURF && sizeof(GT) == 2;
+    constexpr bool kPack = RPL == 2 && !SURF && kPackStore<GT>;
     float ex[RPL], ey[RPL], ez[RPL], dx[RPL], dy[RPL], dz[RPL], t[RPL];
     int env[RPL], pix[RPL];   // env index and r*W + c of each ray (-1: no pixel)
     int taps[RPL];
@@ -692,8 +741,7 @@ __global__ __launch_bounds__(64 * kTileWaves) void march_tiles(MarchArgs a) {
             if (alive[j]) t[j] = fmaxf(s0 * 0.9f, a.min_step);
         }
     }
-    const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(
-        const_cast<void*>(a.grid), 0, (int)a.grid_bytes, kRsrcWord3);
+    const GridReader<GT> rd(a.grid, a.code_bytes, a.hdr_off, a.hdr_bytes);
     const uint32_t* __restrict__ tab = s_axis;
     // Liveness is kept as one 64-bit lane mask per tile (scalar registers):
     // a new mask is the old one ANDed with the ballots of the two compares,
@@ -774,8 +822,8 @@ __global__ __launch_bounds__(64 * kTileWaves) void march_tiles(MarchArgs a) {
                 // a step that stays in the voxel of the ray's previous sample
                 // reuses that value: same voxel, same sample, one line fewer
                 // for the texture path
-                if constexpr (!kReuse) last_sd[j] = load_voxel<GT>(rsrc, off);
-                else if (off != last_off[j]) { last_sd[j] = load_voxel<GT>(rsrc, off); last_off[j] = off; }
+                if constexpr (!kReuse) last_sd[j] = rd(off);
+                else if (off != last_off[j]) { last_sd[j] = rd(off); last_off[j] = off; }
             }
             sd[j] = last_sd[j];
         }
@@ -799,7 +847,7 @@ __global__ __launch_bounds__(64 * kTileWaves) void march_tiles(MarchArgs a) {
             store_enc<OUT_DTYPE>(a.out, o, encode_depth(tc, a.near));
             if constexpr (SURF) {
                 // the voxel the march stopped in (vision.py:176-187, :658-665)
-                constexpr int kLog = sizeof(GT) == 2 ? 1 : 2;
+                constexpr int kLog = kElemLog<GT>;
                 const float px = ex[j] + dx[j] * tc;
                 const float py = ey[j] + dy[j] * tc;
                 const float pz = ez[j] + dz[j] * tc;
@@ -844,8 +892,7 @@ __global__ __launch_bounds__(256) void march_persistent(MarchArgs a) {
     extern __shared__ uint32_t s_axis[];
     fill_axis_tables<GT, LAYOUT>(a, s_axis);
     const int lane = threadIdx.x & 63;
-    const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(
-        const_cast<void*>(a.grid), 0, (int)a.grid_bytes, kRsrcWord3);
+    const GridReader<GT> rd(a.grid, a.code_bytes, a.hdr_off, a.hdr_bytes);
 
     int part = (int)((int64_t)xcd_logical_block(blockIdx.x, a.nblocks) * kParts / a.nblocks);
     uint32_t pending = claim_raw(a, part, lane);   // raw claim on `part`, checked when needed
@@ -936,7 +983,7 @@ __global__ __launch_bounds__(256) void march_persistent(MarchArgs a) {
             if (!more && __ballot(has) == 0) break;
         }
         if (alive) {
-            alive = march_step<GT>(a, rsrc, s_axis, ex, ey, ez, dx, dy, dz, t);
+            alive = march_step<GT>(a, rd, s_axis, ex, ey, ez, dx, dy, dz, t);
             ++k;
             alive = alive && k < a.max_steps;
         }
@@ -948,139 +995,6 @@ __global__ __launch_bounds__(256) void march_persistent(MarchArgs a) {
         if (done == total - 1) {
             for (int p = 0; p < kParts; ++p) atomicExch(&a.counters[p * kCtrStride], 0u);
             atomicExch(&a.counters[kParts * kCtrStride], 0u);
-        }
-    }
-}
-
-// ------------------------------------------------------ schedule: slots --
-// A grid that fills every CU once; each wave marches R independent 8x8 pixel
-// tiles ("slots"), one ray per lane per slot. A slot whose 64 rays have all
-// ended writes them and takes the wave's next tile, so a wave keeps R
-// coherent gathers in flight until its tiles are done: the tiles schedule's
-// coherence without its coupling of R tiles to the slowest ray among them.
-// Tiles are dealt statically: the waves of XCD x (blocks x, x+8, ...) stride
-// through the x-th eighth of the tile range in step, so an XCD works on a
-// few consecutive envs at a time; no atomics, no counters.
-struct TileSource {
-    int next;    // the wave's next tile
-    int stride;  // waves sharing the partition
-    int end;     // end of the partition
-};
-
-__device__ __forceinline__ int take_tile(TileSource& src) {
-    if (src.next >= src.end) return -1;
-    const int tile = src.next;
-    src.next += src.stride;
-    return tile;
-}
-
-__device__ __forceinline__ float uniform_f(float v) {
-    return __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(v)));
-}
-
-template <typename GT, int LAYOUT, int OUT_DTYPE, int CAMERA, bool CENSUS, int R>
-__global__ __launch_bounds__(256) void march_slots(MarchArgs a) {
-    extern __shared__ uint32_t s_axis[];
-    fill_axis_tables<GT, LAYOUT>(a, s_axis);
-    const int lane = threadIdx.x & 63;
-    const int lr = lane >> 3, lc = lane & 7;
-    const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(
-        const_cast<void*>(a.grid), 0, (int)a.grid_bytes, kRsrcWord3);
-    const uint32_t* __restrict__ tab = s_axis;
-    // this wave's place among the waves of its XCD's partition
-    const int total = (int)a.total_tiles;
-    TileSource src;
-    {
-        const int q = a.nblocks >> 3, rem = a.nblocks & 7;
-        const int x = (int)(blockIdx.x & 7);
-        const int nb = q + (x < rem ? 1 : 0);            // blocks on this partition
-        const int lw = (int)(blockIdx.x >> 3) * 4 + (int)(threadIdx.x >> 6);
-        const int lo = (int)((int64_t)total * x / kParts);
-        src.end = (int)((int64_t)total * (x + 1) / kParts);
-        src.next = __builtin_amdgcn_readfirstlane(lo + lw);
-        src.stride = nb * 4;
-    }
-
-    // per slot: wave-uniform eye, tile and step count (scalar registers),
-    // per-lane direction, depth and liveness
-    float ex[R], ey[R], ez[R], dx[R], dy[R], dz[R], t[R];
-    bool alive[R];
-    int tl[R], steps[R], taps[R];
-    auto start = [&](int j) {
-        tl[j] = take_tile(src);
-        if (tl[j] < 0) return;
-        const int n = tl[j] / a.tiles_per_env;
-        const int rem = tl[j] - n * a.tiles_per_env;
-        const int ty = rem / a.tiles_x;
-        const int r = ty * 8 + lr, c = (rem - ty * a.tiles_x) * 8 + lc;
-        const float2* rt = a.rt + (int64_t)n * a.rt_stride;
-        const float2 e01 = rt[a.H + a.W], e2 = rt[a.H + a.W + 1];
-        float2 psc = make_float2(0.f, 0.f), ysc = make_float2(0.f, 0.f);
-        if constexpr (CAMERA == SDFR_CAM_PINHOLE) {
-            psc = rt[a.H + a.W + 2];
-            ysc = rt[a.H + a.W + 3];
-        }
-        const float3 d = ray_dir<CAMERA>(rt[min(r, a.H - 1)], rt[a.H + min(c, a.W - 1)], psc, ysc);
-        ex[j] = uniform_f(e01.x);
-        ey[j] = uniform_f(e01.y);
-        ez[j] = uniform_f(e2.x);
-        dx[j] = d.x;
-        dy[j] = d.y;
-        dz[j] = d.z;
-        t[j] = 0.0f;
-        taps[j] = 0;
-        steps[j] = 0;
-        alive[j] = r < a.H && c < a.W && a.max_steps > 0;
-    };
-    // slot j's rays have all ended: write them
-    auto finish = [&](int j) {
-        const int n = tl[j] / a.tiles_per_env;
-        const int rem = tl[j] - n * a.tiles_per_env;
-        const int ty = rem / a.tiles_x;
-        const int r = ty * 8 + lr, c = (rem - ty * a.tiles_x) * 8 + lc;
-        if (r < a.H && c < a.W) {
-            const int pix = r * a.W + c;
-            const int64_t o = (int64_t)n * a.env_stride + pix;
-            store_enc<OUT_DTYPE>(a.out, o, encode_depth(fminf(t[j], a.rng), a.near));
-            if constexpr (CENSUS) a.taps[(int64_t)n * a.H * a.W + pix] = taps[j];
-        }
-    };
-#pragma unroll
-    for (int j = 0; j < R; ++j) start(j);
-    while (true) {
-        bool any_act = false;
-#pragma unroll
-        for (int j = 0; j < R; ++j) any_act |= tl[j] >= 0;
-        if (!any_act) break;
-        float sd[R];
-#pragma unroll
-        for (int j = 0; j < R; ++j) {
-            sd[j] = 0.0f;
-            if (tl[j] >= 0) {
-                const float px = ex[j] + dx[j] * t[j];
-                const float py = ey[j] + dy[j] * t[j];
-                const float pz = ez[j] + dz[j] * t[j];
-                const int ix = (int)__builtin_amdgcn_fmed3f((px - a.mnx) * a.inv_cell, 0.0f, a.fnx1);
-                const int iy = (int)__builtin_amdgcn_fmed3f((py - a.mny) * a.inv_cell, 0.0f, a.fny1);
-                const int iz = (int)__builtin_amdgcn_fmed3f((pz - a.mnz) * a.inv_cell, 0.0f, a.fnz1);
-                const uint32_t off = alive[j] ? tab[ix] + tab[a.nx + iy] + tab[a.nx + a.ny + iz] : a.dead_off;
-                sd[j] = load_voxel<GT>(rsrc, off);
-            }
-        }
-#pragma unroll
-        for (int j = 0; j < R; ++j) {
-            if (tl[j] < 0) continue;
-            if (alive[j]) {
-                if constexpr (CENSUS) ++taps[j];
-                alive[j] = (sd[j] > a.hit_eps) && (t[j] < a.rng);
-                if (alive[j]) t[j] = t[j] + fmaxf(sd[j] * 0.9f, a.min_step);
-            }
-            ++steps[j];
-            if (steps[j] >= a.max_steps) alive[j] = false;
-            if (!__any(alive[j])) {
-                finish(j);
-                start(j);
-            }
         }
     }
 }
@@ -1145,6 +1059,50 @@ __global__ __launch_bounds__(256) void relayout_grid(const ST* __restrict__ src,
     }
 }
 
+// r16 bricks: one wave per 4x4x4 brick, lane i holding voxel (i&3, (i>>2)&3,
+// i>>4) of it. base = the smallest value of the brick's voxels inside the
+// grid; scale = 2^e for the smallest e >= -100 with (max - base) <= 65535*2^e
+// (e <= 100); code = the value's offset from base in units of scale, rounded
+// to nearest even, in [0, 65535]. Offsets and products are formed in fp64
+// (exact for the values of a distance field). Padding voxels (never
+// addressed) get code 0.
+template <typename ST>
+__global__ __launch_bounds__(256) void encode_r16(const ST* __restrict__ src, uint16_t* __restrict__ codes,
+                                                  float2* __restrict__ hdr, int nx, int ny, int nz, int bx,
+                                                  int by, int64_t n_bricks) {
+    const int64_t brick = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (brick >= n_bricks) return;   // the whole wave leaves together
+    const int lane = threadIdx.x & 63;
+    const int64_t bxy = (int64_t)bx * by;
+    const int bz_i = (int)(brick / bxy);
+    const int by_i = (int)((brick % bxy) / bx);
+    const int bx_i = (int)(brick % bx);
+    const int ix = bx_i * 4 + (lane & 3), iy = by_i * 4 + ((lane >> 2) & 3), iz = bz_i * 4 + (lane >> 4);
+    const bool inside = ix < nx && iy < ny && iz < nz;
+    float v = 0.0f;
+    if (inside) {
+        const int64_t si = ((int64_t)iz * ny + iy) * nx + ix;
+        if constexpr (sizeof(ST) == 2) v = __half2float(((const __half*)src)[si]);
+        else v = ((const float*)src)[si];
+    }
+    float lo = inside ? v : INFINITY, hi = inside ? v : -INFINITY;
+    for (int m = 1; m < 64; m <<= 1) {
+        lo = fminf(lo, __shfl_xor(lo, m));
+        hi = fmaxf(hi, __shfl_xor(hi, m));
+    }
+    const double range = (double)hi - (double)lo;
+    int e = -100;
+    if (range > 0.0) {
+        e = ilogb(range) - 15;               // 2^15 <= range / 2^e < 2^16
+        if (ldexp(range, -e) > 65535.0) ++e;
+        e = e < -100 ? -100 : (e > 100 ? 100 : e);
+    }
+    double q = rint(((double)v - (double)lo) * ldexp(1.0, -e));
+    q = q >= 0.0 ? (q > 65535.0 ? 65535.0 : q) : 0.0;   // NaN -> 0
+    codes[brick * 64 + lane] = inside ? (uint16_t)q : (uint16_t)0;
+    if (lane == 0) hdr[brick] = make_float2(lo, ldexpf(1.0f, e));
+}
+
 template <typename ST, typename DT>
 hipError_t launch_relayout(const void* src, void* dst, const SdfrGrid* g, int64_t count,
                            hipStream_t st) {
@@ -1158,123 +1116,109 @@ hipError_t launch_relayout(const void* src, void* dst, const SdfrGrid* g, int64_
     return hipGetLastError();
 }
 
+// The copy read back as fp32 [nz][ny][nx], one thread per voxel, through the
+// same axis offsets and reader the march uses.
+template <typename GT>
+__global__ __launch_bounds__(256) void read_grid(MarchArgs a, float* __restrict__ out, int64_t n) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    const int ix = (int)(i % a.nx), iy = (int)((i / a.nx) % a.ny), iz = (int)(i / ((int64_t)a.nx * a.ny));
+    constexpr int kLog = kElemLog<GT>;
+    const uint32_t off = axis_offset(ix, a.nx, a.ny, a.layout, a.bx, a.by, kLog) +
+                         axis_offset(a.nx + iy, a.nx, a.ny, a.layout, a.bx, a.by, kLog) +
+                         axis_offset(a.nx + a.ny + iz, a.nx, a.ny, a.layout, a.bx, a.by, kLog);
+    out[i] = GridReader<GT>(a.grid, a.code_bytes, a.hdr_off, a.hdr_bytes)(off);
+}
+
 // --------------------------------------------------------- render dispatch --
 size_t axis_lds_bytes(const MarchArgs& a) {
     return sizeof(uint32_t) * (size_t)(a.nx + a.ny + a.nz);
 }
 
-// The rays per lane (tiles) or slots per wave (slots) a render of `tiles`
-// 8x8 tiles runs with: the handle's setting, or by default 1 for grids
-// beyond the Infinity Cache (fewer rays in flight, fewer misses) and for
-// small renders, else 2.
+// The rays per lane a render of `tiles` 8x8 tiles runs with: the handle's
+// setting, or by default 1 for grids beyond the Infinity Cache (fewer rays in
+// flight, fewer misses) and for small renders, else 2.
 int render_rpl(const SdfrGrid* g, int64_t tiles) {
     if (g->rays_per_lane > 0) return g->rays_per_lane;
     return (g->bytes > kCacheResidentBytes || tiles < kSmallRenderTiles) ? 1 : 2;
 }
 
+// One march launch, chosen and sized before anything is enqueued, so that a
+// render that cannot launch fails before its ray-setup launch has counted
+// tiles into the handle's bucket counts.
+struct MarchPlan {
+    void (*kernel)(MarchArgs);
+    int64_t blocks;
+    int threads;
+    size_t lds;
+};
+
 template <typename GT, int LAYOUT, int OUT, int CAMERA, bool CENSUS, bool SURF>
-void launch_tiles(MarchArgs& a, const SdfrGrid* g, hipStream_t st) {
-    const int rpl = a.rpl;
+MarchPlan plan_tiles(MarchArgs& a, const SdfrGrid* g) {
     size_t lds = axis_lds_bytes(a);
     if (g->bytes > kCacheResidentBytes && g->lds_per_cu > 0)
         lds = max(lds, (size_t)g->lds_per_cu / kSpillBlocksPerCU);   // cap the workgroups per CU
-    const int per_block = kTileWaves * rpl;
-    a.nblocks = (int)((a.logical_tiles + per_block - 1) / per_block);
-    // slot packing (fp16 grids, 2 rays per lane, no surf channel): two
+    const int per_block = kTileWaves * a.rpl;
+    const int64_t blocks = (a.logical_tiles + per_block - 1) / per_block;
+    // slot packing (2-byte stores, 2 rays per lane, no surf channel): two
     // 64-entry lane lists per wave after the axis tables
     a.pack_off = (a.nx + a.ny + a.nz + 63) & ~63;
-    const bool pack = rpl == 2 && !SURF && sizeof(GT) == 2;
-    const size_t lds_pack = pack ? max(lds, sizeof(uint32_t) * ((size_t)a.pack_off + 128 * kTileWaves)) : lds;
-    if (rpl == 2)
-        march_tiles<GT, LAYOUT, OUT, CAMERA, CENSUS, 2, SURF><<<a.nblocks, 64 * kTileWaves, lds_pack, st>>>(a);
-    else
-        march_tiles<GT, LAYOUT, OUT, CAMERA, CENSUS, 1, SURF><<<a.nblocks, 64 * kTileWaves, lds, st>>>(a);
-}
-
-// A grid that fills every CU once (never more waves than tiles) for a
-// schedule whose waves drain the per-XCD tile stream.
-template <typename K>
-int persistent_blocks(K kernel, const MarchArgs& a, const SdfrGrid* g, size_t lds, int tiles_per_wave) {
-    int per_cu = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, reinterpret_cast<const void*>(kernel), 256,
-                                                     lds) != hipSuccess ||
-        per_cu <= 0)
-        per_cu = 1;
-    const int64_t want = (int64_t)per_cu * (g->cus > 0 ? g->cus : 1);
-    const int64_t need = (a.total_tiles + 4 * tiles_per_wave - 1) / (4 * tiles_per_wave);
-    // at least one block per XCD partition: every partition's tiles need waves
-    return (int)(want < need ? (want > 8 ? want : 8) : (need > 8 ? need : 8));
+    const bool pack = a.rpl == 2 && !SURF && kPackStore<GT>;
+    if (pack) lds = max(lds, sizeof(uint32_t) * ((size_t)a.pack_off + 128 * kTileWaves));
+    if (a.rpl == 2)
+        return {march_tiles<GT, LAYOUT, OUT, CAMERA, CENSUS, 2, SURF>, blocks, 64 * kTileWaves, lds};
+    return {march_tiles<GT, LAYOUT, OUT, CAMERA, CENSUS, 1, SURF>, blocks, 64 * kTileWaves, lds};
 }
 
 template <typename GT, int LAYOUT, int OUT, int CAMERA, bool CENSUS>
-void launch_slots(MarchArgs& a, const SdfrGrid* g, size_t lds, hipStream_t st) {
-    switch (a.rpl) {
-    case 1:
-        a.nblocks = persistent_blocks(march_slots<GT, LAYOUT, OUT, CAMERA, CENSUS, 1>, a, g, lds, 1);
-        march_slots<GT, LAYOUT, OUT, CAMERA, CENSUS, 1><<<a.nblocks, 256, lds, st>>>(a);
-        break;
-    case 2:
-        a.nblocks = persistent_blocks(march_slots<GT, LAYOUT, OUT, CAMERA, CENSUS, 2>, a, g, lds, 2);
-        march_slots<GT, LAYOUT, OUT, CAMERA, CENSUS, 2><<<a.nblocks, 256, lds, st>>>(a);
-        break;
-    case 3:
-        a.nblocks = persistent_blocks(march_slots<GT, LAYOUT, OUT, CAMERA, CENSUS, 3>, a, g, lds, 3);
-        march_slots<GT, LAYOUT, OUT, CAMERA, CENSUS, 3><<<a.nblocks, 256, lds, st>>>(a);
-        break;
-    default:
-        a.nblocks = persistent_blocks(march_slots<GT, LAYOUT, OUT, CAMERA, CENSUS, 4>, a, g, lds, 4);
-        march_slots<GT, LAYOUT, OUT, CAMERA, CENSUS, 4><<<a.nblocks, 256, lds, st>>>(a);
-        break;
-    }
-}
-
-template <typename GT, int LAYOUT, int OUT, int CAMERA, bool CENSUS>
-void launch_march(MarchArgs& a, const SdfrGrid* g, bool surf, hipStream_t st) {
+MarchPlan plan_march(MarchArgs& a, const SdfrGrid* g, bool surf) {
     if (surf) {
         // the surf-mask variant exists for the equiangular camera only
         // (vision.py:463-467) and always runs the tiles schedule
-        if constexpr (CAMERA == SDFR_CAM_EQUIANGULAR) {
-            launch_tiles<GT, LAYOUT, OUT, CAMERA, CENSUS, true>(a, g, st);
-        }
-        return;
+        if constexpr (CAMERA == SDFR_CAM_EQUIANGULAR) return plan_tiles<GT, LAYOUT, OUT, CAMERA, CENSUS, true>(a, g);
+        return {nullptr, 0, 0, 0};
     }
-    if (g->schedule == SDFR_SCHED_TILES) {
-        launch_tiles<GT, LAYOUT, OUT, CAMERA, CENSUS, false>(a, g, st);
-        return;
-    }
+    if (g->schedule == SDFR_SCHED_TILES) return plan_tiles<GT, LAYOUT, OUT, CAMERA, CENSUS, false>(a, g);
+    // persistent: a grid that fills every CU once, never more blocks than the tiles need
     const size_t lds = axis_lds_bytes(a);
-    if (g->schedule == SDFR_SCHED_SLOTS) {
-        launch_slots<GT, LAYOUT, OUT, CAMERA, CENSUS>(a, g, lds, st);
-        return;
-    }
-    // a grid that fills every CU once, never more blocks than the tiles need
+    auto k = march_persistent<GT, LAYOUT, OUT, CAMERA, CENSUS>;
     int per_cu = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(
-            &per_cu, reinterpret_cast<const void*>(march_persistent<GT, LAYOUT, OUT, CAMERA, CENSUS>),
-            256, lds) != hipSuccess || per_cu <= 0)
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, reinterpret_cast<const void*>(k), 256,
+                                                     lds) != hipSuccess || per_cu <= 0)
         per_cu = 1;
     const int64_t want = (int64_t)per_cu * (g->cus > 0 ? g->cus : 1);
     const int64_t need = (a.total_tiles + 3) / 4;
-    a.nblocks = (int)(want < need ? want : need);
-    march_persistent<GT, LAYOUT, OUT, CAMERA, CENSUS><<<a.nblocks, 256, lds, st>>>(a);
+    return {k, want < need ? want : need, 256, lds};
 }
 
 template <typename GT, int LAYOUT, int OUT>
-void dispatch_cam(MarchArgs& a, const SdfrGrid* g, bool census, bool surf, hipStream_t st) {
-    if (a.camera == SDFR_CAM_PINHOLE) {
-        if (census) launch_march<GT, LAYOUT, OUT, SDFR_CAM_PINHOLE, true>(a, g, surf, st);
-        else launch_march<GT, LAYOUT, OUT, SDFR_CAM_PINHOLE, false>(a, g, surf, st);
-    } else {
-        if (census) launch_march<GT, LAYOUT, OUT, SDFR_CAM_EQUIANGULAR, true>(a, g, surf, st);
-        else launch_march<GT, LAYOUT, OUT, SDFR_CAM_EQUIANGULAR, false>(a, g, surf, st);
-    }
+MarchPlan plan_cam(MarchArgs& a, const SdfrGrid* g, bool census, bool surf) {
+    if (a.camera == SDFR_CAM_PINHOLE)
+        return census ? plan_march<GT, LAYOUT, OUT, SDFR_CAM_PINHOLE, true>(a, g, surf)
+                      : plan_march<GT, LAYOUT, OUT, SDFR_CAM_PINHOLE, false>(a, g, surf);
+    return census ? plan_march<GT, LAYOUT, OUT, SDFR_CAM_EQUIANGULAR, true>(a, g, surf)
+                  : plan_march<GT, LAYOUT, OUT, SDFR_CAM_EQUIANGULAR, false>(a, g, surf);
 }
 
 template <typename GT, int LAYOUT>
-void dispatch_out(MarchArgs& a, const SdfrGrid* g, int out_dtype, bool census, bool surf,
-                  hipStream_t st) {
-    if (out_dtype == SDFR_BF16) dispatch_cam<GT, LAYOUT, SDFR_BF16>(a, g, census, surf, st);
-    else dispatch_cam<GT, LAYOUT, SDFR_F32>(a, g, census, surf, st);
+MarchPlan plan_out(MarchArgs& a, const SdfrGrid* g, int out_dtype, bool census, bool surf) {
+    return out_dtype == SDFR_BF16 ? plan_cam<GT, LAYOUT, SDFR_BF16>(a, g, census, surf)
+                                  : plan_cam<GT, LAYOUT, SDFR_F32>(a, g, census, surf);
+}
+
+MarchPlan plan_render(MarchArgs& a, const SdfrGrid* g, int out_dtype, bool census, bool surf) {
+    if (g->store_dtype == SDFR_R16) return plan_out<R16, SDFR_LAYOUT_BRICK4>(a, g, out_dtype, census, surf);
+    if (g->store_dtype == SDFR_F16)
+        return g->layout == SDFR_LAYOUT_BRICK4 ? plan_out<__half, SDFR_LAYOUT_BRICK4>(a, g, out_dtype, census, surf)
+                                               : plan_out<__half, SDFR_LAYOUT_LINEAR>(a, g, out_dtype, census, surf);
+    return g->layout == SDFR_LAYOUT_BRICK4 ? plan_out<float, SDFR_LAYOUT_BRICK4>(a, g, out_dtype, census, surf)
+                                           : plan_out<float, SDFR_LAYOUT_LINEAR>(a, g, out_dtype, census, surf);
+}
+
+// Clears n words (the tile order's bucket counts) with ordinary vector
+// stores: a kernel, not a memset node, so that a caller may capture it.
+__global__ __launch_bounds__(256) void clear_words(uint32_t* p, int n) {
+    for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) p[i] = 0u;
 }
 
 bool dtype_ok_for_ducked(int d) {
@@ -1353,6 +1297,161 @@ int64_t workspace_bytes(int width, int height, int n_envs) {
            align256(tiles * (int64_t)sizeof(uint16_t)) + align256(tiles * (int64_t)sizeof(uint32_t));
 }
 
+// The grid's part of the kernel arguments.
+void set_grid_args(MarchArgs* a, const SdfrGrid* grid) {
+    a->grid = grid->data;
+    a->code_bytes = (uint32_t)grid->code_bytes;
+    const bool r16 = grid->store_dtype == SDFR_R16;
+    a->hdr_off = r16 ? (uint32_t)grid->hdr_off : 0u;
+    a->hdr_bytes = r16 ? (uint32_t)(grid->bytes - grid->hdr_off) : 0u;
+    a->store = grid->store_dtype;
+    a->nx = grid->desc.nx;
+    a->ny = grid->desc.ny;
+    a->nz = grid->desc.nz;
+    a->bx = grid->bx;
+    a->by = grid->by;
+    a->layout = grid->layout;
+    a->fnx1 = (float)(grid->desc.nx - 1);
+    a->fny1 = (float)(grid->desc.ny - 1);
+    a->fnz1 = (float)(grid->desc.nz - 1);
+    a->mnx = grid->desc.mins[0];
+    a->mny = grid->desc.mins[1];
+    a->mnz = grid->desc.mins[2];
+    a->inv_cell = (float)(1.0 / (double)grid->desc.cell);   // Python's 1.0/cell, then fp32
+}
+
+// The render behind sdfr_render. Everything that can be refused is checked
+// and the march launch is planned before the first launch is enqueued. After
+// the ray-setup launch has counted tiles into the handle's bucket counts, only
+// the march clears them; if a later step fails, the counts are cleared by a
+// small kernel, or, if even that cannot be launched, by the next render on the
+// handle before its own ray setup (hist_dirty). So a failed render never
+// leaves counts that would misplace the next render's tiles.
+int32_t render_impl(const char* fn, const SdfrGrid* grid, const SdfrCam* cam, const SdfrPoses* poses,
+                    const SdfrImage* image, void* workspace, int64_t workspace_size, void* stream) {
+    if (!grid || !grid->data) return fail(-1, "%s: null grid handle", fn);
+    if (!image) return fail(-1, "%s: null image argument", fn);
+    int32_t rc = check_cam_poses(fn, cam, poses);
+    if (rc) return rc;
+    if (!image->out) return fail(-1, "%s: null output pointer", fn);
+    if (image->dtype != SDFR_F32 && image->dtype != SDFR_BF16)
+        return fail(-3, "%s: output dtype must be f32 or bf16 (got %d)", fn, image->dtype);
+    if (image->channels != 1 && image->channels != 2)
+        return fail(-3, "%s: channels must be 1 or 2 (got %d)", fn, image->channels);
+    const bool surf = image->channels == 2;
+    if (surf && !grid->nz_data)
+        return fail(-1, "%s: 2 channels need a surf-mask grid (sdfr_grid_attach_surfnz)", fn);
+    if (surf && cam->camera != SDFR_CAM_EQUIANGULAR)
+        return fail(-3, "%s: the surf-mask channel has no pinhole kernel", fn);
+    if (image->env_stride < (int64_t)cam->width * cam->height * image->channels)
+        return fail(-2, "%s: env_stride %lld is smaller than H*W*channels", fn,
+                    (long long)image->env_stride);
+    const int64_t need = workspace_bytes(cam->width, cam->height, poses->n_envs);
+    if (!workspace || workspace_size < need)
+        return fail(-2, "%s: workspace of %lld bytes needed (got %lld)", fn, (long long)need,
+                    (long long)workspace_size);
+    if (((uintptr_t)workspace & 7u) != 0) return fail(-2, "%s: workspace must be 8-byte aligned", fn);
+
+    MarchArgs a;
+    fill_args(&a, cam, poses);
+    a.rt = (float2*)workspace;
+    set_grid_args(&a, grid);
+    a.out = image->out;
+    a.env_stride = image->env_stride;
+    a.taps = image->taps;
+    a.counters = grid->counters;
+    a.refill_lanes = grid->refill_lanes;
+    a.nzmask = grid->nz_data;
+    a.nz_bytes = (uint32_t)grid->nz_bytes;
+    a.tiles_x = (cam->width + 7) / 8;
+    a.tiles_per_env = a.tiles_x * ((cam->height + 7) / 8);
+    a.total_tiles = (int64_t)a.tiles_per_env * poses->n_envs;
+    a.perm = nullptr;
+    a.order_hist = nullptr;
+    a.order_key = nullptr;
+    a.order_rank = nullptr;
+    a.order_shift = 0;
+    a.lookahead = (grid->bytes > kCacheResidentBytes ? kOrderLookaheadSpilled : kOrderLookahead) *
+                  cam->near;
+    a.rpl = render_rpl(grid, a.total_tiles);
+    a.order_unit = kTileWaves * a.rpl;
+    a.order_units = (a.total_tiles + a.order_unit - 1) / a.order_unit;
+    a.logical_tiles = a.total_tiles;
+    if (grid->tile_order == SDFR_ORDER_LOOKAHEAD && (grid->schedule == SDFR_SCHED_TILES || surf) &&
+        a.total_tiles >= grid->order_min_tiles) {
+        uint8_t* ws = (uint8_t*)workspace + ray_table_bytes(cam->width, cam->height, poses->n_envs);
+        a.perm = (int32_t*)ws;
+        ws += align256(a.total_tiles * (int64_t)sizeof(int32_t));
+        a.order_key = (uint16_t*)ws;
+        a.logical_tiles = a.order_units * a.order_unit;
+        ws += align256(a.total_tiles * (int64_t)sizeof(uint16_t));
+        a.order_rank = (uint32_t*)ws;
+        a.order_hist = grid->order_hist;
+        const int maxdim = max(a.nx, max(a.ny, a.nz));
+        while (((maxdim - 1) >> a.order_shift) >= (1 << kOrderCellsLog)) ++a.order_shift;
+    }
+
+    // plan every launch before enqueueing any
+    const bool census = image->taps != nullptr;
+    const MarchPlan plan = plan_render(a, grid, image->dtype, census, surf);
+    if (!plan.kernel) return fail(-3, "%s: no march kernel for this combination", fn);
+    if (plan.blocks < 1 || plan.blocks > 0x7fffffff)
+        return fail(-2, "%s: too many envs (%lld march blocks)", fn, (long long)plan.blocks);
+    if (grid->lds_per_block > 0 && plan.lds > (size_t)grid->lds_per_block)
+        return fail(-2, "%s: the march needs %zu bytes of LDS per workgroup, the device allows %d "
+                    "(nx+ny+nz = %d)", fn, plan.lds, grid->lds_per_block, a.nx + a.ny + a.nz);
+    a.nblocks = (int)plan.blocks;
+    const int64_t entries = (int64_t)poses->n_envs * a.rt_stride;
+    const int64_t table_blocks = (entries + 255) / 256;
+    const int64_t sort_blocks = a.perm ? (a.order_units + kOrderChunk - 1) / kOrderChunk : 0;
+    if (table_blocks + sort_blocks > 0x7fffffff)
+        return fail(-2, "%s: too many envs (%lld ray-setup blocks)", fn,
+                    (long long)(table_blocks + sort_blocks));
+
+    hipStream_t st = (hipStream_t)stream;
+    hipError_t e = hipGetLastError();   // an earlier, unrelated error must not be taken for ours
+    (void)e;
+    if (grid->hist_dirty) {
+        clear_words<<<16, 256, 0, st>>>(grid->order_hist, kOrderBuckets);
+        e = hipGetLastError();
+        if (e != hipSuccess)
+            return fail(-4, "%s: clearing the tile order's counts failed: %s", fn, hipGetErrorString(e));
+        grid->hist_dirty = false;
+    }
+    if (cam->camera == SDFR_CAM_PINHOLE)
+        ray_setup<SDFR_CAM_PINHOLE><<<(int)(table_blocks + sort_blocks), 256, 0, st>>>(a, (int)sort_blocks);
+    else
+        ray_setup<SDFR_CAM_EQUIANGULAR><<<(int)(table_blocks + sort_blocks), 256, 0, st>>>(a, (int)sort_blocks);
+    e = hipGetLastError();
+    if (e != hipSuccess) return fail(-4, "%s: ray setup launch failed: %s", fn, hipGetErrorString(e));
+    // from here on a sorted render has counted into order_hist
+    auto abandon = [&](const char* what, hipError_t err) -> int32_t {
+        if (a.order_hist) {
+            clear_words<<<16, 256, 0, st>>>(grid->order_hist, kOrderBuckets);
+            grid->hist_dirty = hipGetLastError() != hipSuccess;
+        }
+        return fail(-4, "%s: %s failed: %s", fn, what, hipGetErrorString(err));
+    };
+    if (sort_blocks) {
+        order_scatter<<<(int)sort_blocks, 256, 0, st>>>(a);
+        e = hipGetLastError();
+        if (e != hipSuccess) return abandon("tile order launch", e);
+    }
+    if (grid->march_events[0]) {
+        e = hipEventRecord((hipEvent_t)grid->march_events[0], st);
+        if (e != hipSuccess) return abandon("recording the march start event", e);
+    }
+    plan.kernel<<<(int)plan.blocks, plan.threads, plan.lds, st>>>(a);
+    e = hipGetLastError();
+    if (e != hipSuccess) return abandon("march launch", e);
+    if (grid->march_events[1]) {
+        e = hipEventRecord((hipEvent_t)grid->march_events[1], st);
+        if (e != hipSuccess) return fail(-4, "%s: recording the march stop event failed: %s", fn,
+                                         hipGetErrorString(e));
+    }
+    return 0;
+}
+
 }  // namespace
 
 // ================================================================ C ABI ==
@@ -1396,13 +1495,18 @@ SDFR_API SdfrGrid* sdfr_grid_create(const SdfrGridDesc* desc, const void* src, i
         copy_err(err, errlen);
         return nullptr;
     }
-    if (store_dtype != SDFR_F32 && store_dtype != SDFR_F16) {
-        fail(-3, "sdfr_grid_create: store dtype must be f32 or f16 (got %d)", store_dtype);
+    if (store_dtype != SDFR_F32 && store_dtype != SDFR_F16 && store_dtype != SDFR_R16) {
+        fail(-3, "sdfr_grid_create: store dtype must be f32, f16 or r16 (got %d)", store_dtype);
         copy_err(err, errlen);
         return nullptr;
     }
     if (layout != SDFR_LAYOUT_LINEAR && layout != SDFR_LAYOUT_BRICK4) {
         fail(-3, "sdfr_grid_create: unknown layout %d", layout);
+        copy_err(err, errlen);
+        return nullptr;
+    }
+    if (store_dtype == SDFR_R16 && layout != SDFR_LAYOUT_BRICK4) {
+        fail(-3, "sdfr_grid_create: the r16 store exists in the brick4 layout only");
         copy_err(err, errlen);
         return nullptr;
     }
@@ -1417,11 +1521,16 @@ SDFR_API SdfrGrid* sdfr_grid_create(const SdfrGridDesc* desc, const void* src, i
     }
     // The kernels address the copy with 32-bit byte offsets through a buffer
     // descriptor, summed from per-axis tables held in LDS (axis_offset).
-    const int64_t elem = store_dtype == SDFR_F16 ? 2 : 4;
-    if (count * elem > (int64_t)0xffffffffLL ||
+    const int64_t elem = store_dtype == SDFR_F32 ? 4 : 2;
+    const int64_t code_bytes = count * elem;
+    const int64_t n_bricks = count / 64;
+    const int64_t hdr_off = store_dtype == SDFR_R16 ? align256(code_bytes) : 0;
+    const int64_t total_bytes =
+        store_dtype == SDFR_R16 ? hdr_off + n_bricks * (int64_t)sizeof(float2) : code_bytes;
+    if (total_bytes > (int64_t)0xffffffffLL ||
         (int64_t)desc->nx + desc->ny + desc->nz > kMaxAxisEntries) {
         fail(-2, "sdfr_grid_create: grid too large (%d x %d x %d, %lld bytes; limits: 4 GiB and "
-             "nx+ny+nz <= %d)", desc->nx, desc->ny, desc->nz, (long long)(count * elem),
+             "nx+ny+nz <= %d)", desc->nx, desc->ny, desc->nz, (long long)total_bytes,
              kMaxAxisEntries);
         copy_err(err, errlen);
         return nullptr;
@@ -1435,7 +1544,9 @@ SDFR_API SdfrGrid* sdfr_grid_create(const SdfrGridDesc* desc, const void* src, i
     g->bx = bx;
     g->by = by;
     g->bz = bz;
-    g->bytes = count * elem;
+    g->bytes = total_bytes;
+    g->code_bytes = code_bytes;
+    g->hdr_off = hdr_off;
     g->data = nullptr;
     g->counters = nullptr;
     g->nz_data = nullptr;
@@ -1450,11 +1561,17 @@ SDFR_API SdfrGrid* sdfr_grid_create(const SdfrGridDesc* desc, const void* src, i
     g->tile_order = SDFR_ORDER_LOOKAHEAD;
     g->order_min_tiles = kOrderMinTiles;
     g->order_hist = nullptr;
+    g->hist_dirty = false;
+    g->lds_per_block = 0;
+    g->march_events[0] = g->march_events[1] = nullptr;
     hipError_t e = hipGetDevice(&g->device);
     if (e == hipSuccess)
         e = hipDeviceGetAttribute(&g->cus, hipDeviceAttributeMultiprocessorCount, g->device);
     if (e == hipSuccess)
         e = hipDeviceGetAttribute(&g->lds_per_cu, hipDeviceAttributeMaxSharedMemoryPerMultiprocessor,
+                                  g->device);
+    if (e == hipSuccess)
+        e = hipDeviceGetAttribute(&g->lds_per_block, hipDeviceAttributeMaxSharedMemoryPerBlock,
                                   g->device);
 
     const int64_t src_bytes = nvox * (src_dtype == SDFR_F16 ? 2 : 4);
@@ -1471,7 +1588,18 @@ SDFR_API SdfrGrid* sdfr_grid_create(const SdfrGridDesc* desc, const void* src, i
             e = hipMemcpyAsync(staged, src, (size_t)src_bytes, hipMemcpyHostToDevice, st);
         dsrc = staged;
     }
-    if (e == hipSuccess) {
+    if (e == hipSuccess && store_dtype == SDFR_R16) {
+        uint16_t* codes = (uint16_t*)g->data;
+        float2* hdr = (float2*)((char*)g->data + hdr_off);
+        const int blocks = (int)((n_bricks + 3) / 4);
+        if (src_dtype == SDFR_F32)
+            encode_r16<float><<<blocks, 256, 0, st>>>((const float*)dsrc, codes, hdr, desc->nx,
+                                                      desc->ny, desc->nz, bx, by, n_bricks);
+        else
+            encode_r16<__half><<<blocks, 256, 0, st>>>((const __half*)dsrc, codes, hdr, desc->nx,
+                                                       desc->ny, desc->nz, bx, by, n_bricks);
+        e = hipGetLastError();
+    } else if (e == hipSuccess) {
         if (src_dtype == SDFR_F32 && store_dtype == SDFR_F32)
             e = launch_relayout<float, float>(dsrc, g->data, g, count, st);
         else if (src_dtype == SDFR_F32)
@@ -1539,16 +1667,14 @@ SDFR_API int32_t sdfr_grid_set_schedule(SdfrGrid* grid, int32_t schedule, int32_
                                         int32_t rays_per_lane) {
     g_err[0] = '\0';
     if (!grid) return fail(-1, "sdfr_grid_set_schedule: null grid handle");
-    if (schedule != SDFR_SCHED_PERSISTENT && schedule != SDFR_SCHED_TILES &&
-        schedule != SDFR_SCHED_SLOTS)
+    if (schedule != SDFR_SCHED_PERSISTENT && schedule != SDFR_SCHED_TILES)
         return fail(-3, "sdfr_grid_set_schedule: unknown schedule %d", schedule);
     if (refill_lanes < 1 || refill_lanes > 64)
         return fail(-2, "sdfr_grid_set_schedule: refill_lanes must be in 1..64 (got %d)",
                     refill_lanes);
-    const int max_rpl = schedule == SDFR_SCHED_SLOTS ? 4 : 2;
-    if (rays_per_lane < 0 || rays_per_lane > max_rpl)
-        return fail(-2, "sdfr_grid_set_schedule: rays_per_lane must be in 0..%d for this schedule "
-                    "(got %d; 0 = by grid and render size)", max_rpl, rays_per_lane);
+    if (rays_per_lane < 0 || rays_per_lane > 2)
+        return fail(-2, "sdfr_grid_set_schedule: rays_per_lane must be in 0..2 "
+                    "(got %d; 0 = by grid and render size)", rays_per_lane);
     grid->schedule = schedule;
     grid->refill_lanes = refill_lanes;
     grid->rays_per_lane = rays_per_lane;
@@ -1589,120 +1715,28 @@ SDFR_API int32_t sdfr_render(const SdfrGrid* grid, const SdfrCam* cam, const Sdf
                              const SdfrImage* image, void* workspace, int64_t workspace_size,
                              void* stream) {
     g_err[0] = '\0';
-    if (!grid || !grid->data) return fail(-1, "sdfr_render: null grid handle");
-    if (!image) return fail(-1, "sdfr_render: null image argument");
-    int32_t rc = check_cam_poses("sdfr_render", cam, poses);
-    if (rc) return rc;
-    if (!image->out) return fail(-1, "sdfr_render: null output pointer");
-    if (image->dtype != SDFR_F32 && image->dtype != SDFR_BF16)
-        return fail(-3, "sdfr_render: output dtype must be f32 or bf16 (got %d)", image->dtype);
-    if (image->channels != 1 && image->channels != 2)
-        return fail(-3, "sdfr_render: channels must be 1 or 2 (got %d)", image->channels);
-    const bool surf = image->channels == 2;
-    if (surf && !grid->nz_data)
-        return fail(-1, "sdfr_render: 2 channels need a surf-mask grid (sdfr_grid_attach_surfnz)");
-    if (surf && cam->camera != SDFR_CAM_EQUIANGULAR)
-        return fail(-3, "sdfr_render: the surf-mask channel has no pinhole kernel");
-    if (image->env_stride < (int64_t)cam->width * cam->height * image->channels)
-        return fail(-2, "sdfr_render: env_stride %lld is smaller than H*W*channels",
-                    (long long)image->env_stride);
-    const int64_t need = workspace_bytes(cam->width, cam->height, poses->n_envs);
-    if (!workspace || workspace_size < need)
-        return fail(-2, "sdfr_render: workspace of %lld bytes needed (got %lld)", (long long)need,
-                    (long long)workspace_size);
-    if (((uintptr_t)workspace & 7u) != 0)
-        return fail(-2, "sdfr_render: workspace must be 8-byte aligned");
+    return render_impl("sdfr_render", grid, cam, poses, image, workspace, workspace_size, stream);
+}
 
+SDFR_API int32_t sdfr_grid_read(const SdfrGrid* grid, float* out, void* stream) {
+    g_err[0] = '\0';
+    if (!grid || !grid->data) return fail(-1, "sdfr_grid_read: null grid handle");
+    if (!out) return fail(-1, "sdfr_grid_read: null output pointer");
     MarchArgs a;
-    fill_args(&a, cam, poses);
-    a.rt = (float2*)workspace;
-    a.grid = grid->data;
-    a.grid_bytes = (uint32_t)grid->bytes;
-    a.grid_f16 = grid->store_dtype == SDFR_F16;
-    // an offset at the end of the range is out of range for a 4-byte read;
-    // near 4 GiB fall back to offset 0, an ordinary in-range read
-    a.dead_off = grid->bytes <= 0xffffff00ll ? (uint32_t)grid->bytes : 0u;
-    a.nx = grid->desc.nx;
-    a.ny = grid->desc.ny;
-    a.nz = grid->desc.nz;
-    a.bx = grid->bx;
-    a.by = grid->by;
-    a.layout = grid->layout;
-    a.fnx1 = (float)(grid->desc.nx - 1);
-    a.fny1 = (float)(grid->desc.ny - 1);
-    a.fnz1 = (float)(grid->desc.nz - 1);
-    a.mnx = grid->desc.mins[0];
-    a.mny = grid->desc.mins[1];
-    a.mnz = grid->desc.mins[2];
-    a.inv_cell = (float)(1.0 / (double)grid->desc.cell);   // Python's 1.0/cell, then fp32
-    a.out = image->out;
-    a.env_stride = image->env_stride;
-    a.taps = image->taps;
-    a.counters = grid->counters;
-    a.refill_lanes = grid->refill_lanes;
-    a.nzmask = grid->nz_data;
-    a.nz_bytes = (uint32_t)grid->nz_bytes;
-    a.tiles_x = (cam->width + 7) / 8;
-    a.tiles_per_env = a.tiles_x * ((cam->height + 7) / 8);
-    a.total_tiles = (int64_t)a.tiles_per_env * poses->n_envs;
-    const int64_t nblocks = (a.total_tiles + kTileWaves - 1) / kTileWaves;
-    if (nblocks > 0x7fffffff)
-        return fail(-2, "sdfr_render: too many envs (%lld blocks)", (long long)nblocks);
-    a.nblocks = (int)nblocks;
-    a.perm = nullptr;
-    a.order_hist = nullptr;
-    a.order_key = nullptr;
-    a.order_rank = nullptr;
-    a.order_shift = 0;
-    a.lookahead = (grid->bytes > kCacheResidentBytes ? kOrderLookaheadSpilled : kOrderLookahead) *
-                  cam->near;
-    a.rpl = render_rpl(grid, a.total_tiles);
-    a.order_unit = kTileWaves * a.rpl;
-    a.order_units = (a.total_tiles + a.order_unit - 1) / a.order_unit;
-    a.logical_tiles = a.total_tiles;
-    if (grid->tile_order == SDFR_ORDER_LOOKAHEAD && (grid->schedule == SDFR_SCHED_TILES || surf) &&
-        a.total_tiles >= grid->order_min_tiles) {
-        uint8_t* ws = (uint8_t*)workspace + ray_table_bytes(cam->width, cam->height, poses->n_envs);
-        a.perm = (int32_t*)ws;
-        ws += align256(a.total_tiles * (int64_t)sizeof(int32_t));
-        a.order_key = (uint16_t*)ws;
-        a.logical_tiles = a.order_units * a.order_unit;
-        ws += align256(a.total_tiles * (int64_t)sizeof(uint16_t));
-        a.order_rank = (uint32_t*)ws;
-        a.order_hist = grid->order_hist;
-        const int maxdim = max(a.nx, max(a.ny, a.nz));
-        while (((maxdim - 1) >> a.order_shift) >= (1 << kOrderCellsLog)) ++a.order_shift;
-    }
-
+    memset(&a, 0, sizeof a);
+    set_grid_args(&a, grid);
+    const int64_t n = (int64_t)a.nx * a.ny * a.nz;
+    const int64_t blocks = (n + 255) / 256;
+    if (blocks > 0x7fffffff) return fail(-2, "sdfr_grid_read: grid too large");
     hipStream_t st = (hipStream_t)stream;
-    const int64_t entries = (int64_t)poses->n_envs * a.rt_stride;
-    const int table_blocks = (int)((entries + 255) / 256);
-    const int sort_blocks = a.perm ? (int)((a.order_units + kOrderChunk - 1) / kOrderChunk) : 0;
-    if (cam->camera == SDFR_CAM_PINHOLE)
-        ray_setup<SDFR_CAM_PINHOLE><<<table_blocks + sort_blocks, 256, 0, st>>>(a, sort_blocks);
+    if (grid->store_dtype == SDFR_R16)
+        read_grid<R16><<<(int)blocks, 256, 0, st>>>(a, out, n);
+    else if (grid->store_dtype == SDFR_F16)
+        read_grid<__half><<<(int)blocks, 256, 0, st>>>(a, out, n);
     else
-        ray_setup<SDFR_CAM_EQUIANGULAR><<<table_blocks + sort_blocks, 256, 0, st>>>(a, sort_blocks);
-    if (sort_blocks) order_scatter<<<sort_blocks, 256, 0, st>>>(a);
-    const bool census = image->taps != nullptr;
-    if (grid->march_events[0] &&
-        hipEventRecord((hipEvent_t)grid->march_events[0], st) != hipSuccess)
-        return fail(-4, "sdfr_render: recording the march start event failed");
-    if (grid->store_dtype == SDFR_F16) {
-        if (grid->layout == SDFR_LAYOUT_BRICK4)
-            dispatch_out<__half, SDFR_LAYOUT_BRICK4>(a, grid, image->dtype, census, surf, st);
-        else
-            dispatch_out<__half, SDFR_LAYOUT_LINEAR>(a, grid, image->dtype, census, surf, st);
-    } else {
-        if (grid->layout == SDFR_LAYOUT_BRICK4)
-            dispatch_out<float, SDFR_LAYOUT_BRICK4>(a, grid, image->dtype, census, surf, st);
-        else
-            dispatch_out<float, SDFR_LAYOUT_LINEAR>(a, grid, image->dtype, census, surf, st);
-    }
+        read_grid<float><<<(int)blocks, 256, 0, st>>>(a, out, n);
     const hipError_t e = hipGetLastError();
-    if (e != hipSuccess) return fail(-4, "sdfr_render: launch failed: %s", hipGetErrorString(e));
-    if (grid->march_events[1] &&
-        hipEventRecord((hipEvent_t)grid->march_events[1], st) != hipSuccess)
-        return fail(-4, "sdfr_render: recording the march stop event failed");
+    if (e != hipSuccess) return fail(-4, "sdfr_grid_read: launch failed: %s", hipGetErrorString(e));
     return 0;
 }
 

@@ -27,8 +27,8 @@ import torch
 
 from . import _sdfr, vision
 
-__all__ = ["GoalField", "build_goal_field", "goal_field_from_occupancy", "zone_seed_box",
-           "seed_voxel_box"]
+__all__ = ["GoalField", "EuclidField", "build_goal_field", "goal_field_from_occupancy",
+           "zone_seed_box", "seed_voxel_box", "goal_occupancy"]
 
 # the reference's cache versioning (goalfield.py:44-47): a cache written here
 # carries the same signature as one the reference wrote
@@ -188,6 +188,35 @@ class GoalField:
         return yaw.cpu().numpy() if was_np else yaw
 
 
+class EuclidField:
+    """Straight-line distance to the goal box, walls ignored
+    (goalfield.py:110-137): the field of ``--race-dist euclid``, with no bake.
+    Same methods as :class:`GoalField`; every position counts as reachable.
+    Host numpy in and out, as the reference's; a handful of positions per
+    tick is not worth a launch."""
+
+    def __init__(self, zone):
+        self.mins = np.asarray(zone["mins"], np.float64)
+        self.maxs = np.asarray(zone["maxs"], np.float64)
+
+    def _nearest(self, pos):
+        p = np.atleast_2d(np.asarray(pos, np.float64))
+        return p, np.minimum(np.maximum(p, self.mins), self.maxs)   # closest point of the box
+
+    def sample(self, pos) -> np.ndarray:
+        """(N,) float32 distance from each position to the box (0 inside)."""
+        p, q = self._nearest(pos)
+        return np.sqrt(((p - q) ** 2).sum(axis=1)).astype(np.float32)
+
+    def reachable(self, pos) -> np.ndarray:
+        return np.ones(len(np.atleast_2d(pos)), bool)
+
+    def descent_yaw(self, pos) -> np.ndarray:
+        """Yaw in degrees [0, 360) pointing at the box's closest point."""
+        p, q = self._nearest(pos)
+        return np.degrees(np.arctan2(q[:, 1] - p[:, 1], q[:, 0] - p[:, 0])) % 360.0
+
+
 @torch.no_grad()
 def goal_field_from_occupancy(occ, mins, zone, cell: float, device="cuda", *, keep_u16=False,
                               max_sweeps: int = MAX_SWEEPS) -> GoalField:
@@ -248,16 +277,51 @@ def _goal_sig(bsp: Path, zone, mask_kill: bool) -> str:
             f"{_map_sig(bsp)}_" + "_".join(f"{v:g}" for v in box))
 
 
+def goal_occupancy(core, cell: float, cache_dir=None):
+    """The goal graph's occupancy: the vision's slab-catching grid
+    (goalfield.py:140-145)."""
+    return vision.slab_occupancy(core, cell, cache_dir)
+
+
+def _mask_kill_volumes(occ, mins, cell: float, bsp: Path):
+    """Kill volumes as walls of the goal graph only (goalfield.py:188-219):
+    the voxel centres inside each kill trigger's hull, classified by the
+    package's BSP hull probe (``zones.kill_zones`` / ``zones.hull_probe``),
+    become solid. The trigger's box (grown by 1 u) bounds the voxels tested."""
+    zones = vision._sibling("zones")
+    occ = np.array(occ, copy=True)
+    gz, gy, gx = occ.shape
+    inside_hull = zones.hull_probe(bsp)
+    kills = zones.kill_zones(bsp)
+    walled = 0
+    for k in kills:
+        lo_u = np.asarray(k["mins"], np.float64) - 1.0
+        hi_u = np.asarray(k["maxs"], np.float64) + 1.0
+        lo = np.maximum(np.floor((lo_u - mins) / cell - 0.5), 0).astype(int)
+        hi = np.minimum(np.ceil((hi_u - mins) / cell - 0.5) + 1, [gx, gy, gz]).astype(int)
+        if (hi <= lo).any():
+            continue
+        axes = [mins[a] + (np.arange(lo[a], hi[a]) + 0.5) * cell for a in range(3)]
+        zz, yy, xx = np.meshgrid(axes[2], axes[1], axes[0], indexing="ij")
+        pts = np.stack([xx.ravel(), yy.ravel(), zz.ravel()], 1)
+        hit = inside_hull(int(k["model"][1:]), pts - np.asarray(k["origin"], np.float64))
+        if hit.any():
+            box = occ[lo[2]:hi[2], lo[1]:hi[1], lo[0]:hi[0]]
+            m = np.asarray(hit).reshape(box.shape)
+            walled += int((m & (box == 0)).sum())
+            box[m] = 1
+    print(f"goal graph: {len(kills)} kill volumes hull-masked ({walled} free voxels -> wall)")
+    return occ
+
+
 def build_goal_field(core, zone, cell: float, cache_dir=None, device="cuda",
                      mask_kill: bool = False) -> GoalField:
     """Build (or load) the geodesic field toward ``zone`` (goalfield.py:159-298).
 
-    Loads ``<map>.goal_<cell>.npz`` when its signature is current, as the
-    reference does. Otherwise bakes on the GPU from the map's slab occupancy
-    cache ``<map>.slabocc_<cell>.npz`` (vision.py:346-369; sampling that
-    occupancy needs the reference's BSP core, which this package does not
-    carry) and writes the goal cache in the reference's format. Kill-volume
-    masking needs the BSP hull probes and is only available from a cache.
+    Loads ``<map>.goal[k]_<cell>.npz`` when its signature is current, as the
+    reference does. Otherwise bakes on the GPU from :func:`goal_occupancy`
+    (with ``mask_kill``, kill volumes walled off first) and writes the goal
+    cache in the reference's format.
     """
     bsp = Path(core.bsp_path)
     sig = _goal_sig(bsp, zone, mask_kill)
@@ -268,13 +332,15 @@ def build_goal_field(core, zone, cell: float, cache_dir=None, device="cuda",
         if "sig" in z and str(z["sig"]) == sig:
             return GoalField(z["grid"], z["mins"], float(z["cell"]), float(z["reach_max"]),
                              quant=float(z["quant"]), device=device)
+    occ, mins = goal_occupancy(core, cell, cache_dir)
     if mask_kill:
-        raise NotImplementedError("kill-volume masking needs the reference's BSP hull probes; "
-                                  "bake that goal field with the reference")
-    occ, mins = vision.slab_occupancy(core, cell, cache_dir)
+        occ = _mask_kill_volumes(occ, np.asarray(mins, np.float64), cell, bsp)
     field = goal_field_from_occupancy(occ, mins, zone, cell, device=device)
+    info = field.bake_info
+    print(f"goal field: {info['sweeps']} sweeps, {info['n_seed']} seed voxels, "
+          f"max geodesic {field.reach_max:.0f}u")
     q = field.grid_q.cpu().numpy().view(np.uint16)
-    np.savez_compressed(cache_file, grid=q, quant=np.float32(field.bake_info["quant"]),
+    np.savez_compressed(cache_file, grid=q, quant=np.float32(info["quant"]),
                         mins=mins, cell=np.float32(cell),
                         reach_max=np.float32(field.reach_max), sig=np.str_(sig))
     return field

@@ -23,10 +23,13 @@ sparse_grazing      256x256x128 @16 u, 16 ramps,  8192     256     6144 / 2000
                     pitch N(0,5 deg)
 ramp_field_f16_bf16 ramp_field scene stored f16,  8192     96      6144 / 2000
                     bf16 output
+ramp_field_r16_bf16 ramp_field scene stored as    8192     96      6144 / 2000
+                    r16 bricks, bf16 output
 =================== ============================ ======== ======= ===========
 
 hit_eps is 1 u in every workload. Scene seeds are 1000+k and pose seeds
-2000+k (numpy PCG64) for the k-th row above.
+2000+k (numpy PCG64) for the k-th row above; the two fused-output rows share
+scene and poses (seed 2004) and differ only in the grid store.
 """
 from __future__ import annotations
 
@@ -342,6 +345,10 @@ WORKLOADS = {
         "ramp_field_f16_bf16", _field_scene, lambda s, n: poses_above_ramps(s, n, 2004),
         n_envs=8192, max_steps=96, range_units=6144.0, near_range=2000.0,
         store="f16", out_dtype="bf16"),
+    "ramp_field_r16_bf16": Workload(
+        "ramp_field_r16_bf16", _field_scene, lambda s, n: poses_above_ramps(s, n, 2004),
+        n_envs=8192, max_steps=96, range_units=6144.0, near_range=2000.0,
+        store="r16", out_dtype="bf16"),
 }
 
 

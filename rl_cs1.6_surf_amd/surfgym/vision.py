@@ -31,7 +31,8 @@ __all__ = ["GpuLidar", "build_sdf", "sdf_from_occupancy", "map_occupancy", "slab
            "pick_cell", "grid_dims", "SOLID_ENT_CLASSES"]
 
 # brush entities the reference's physics collides with (vision.py:301-307);
-# kept for importers of the name, the bake itself is not part of this module
+# thin ones are rasterised into the slab occupancy, and the surfability bake
+# imports the name
 SOLID_ENT_CLASSES = {"func_wall", "func_breakable", "func_pushable",
                      "func_button", "func_train", "func_conveyor",
                      "func_wall_toggle", "func_rotating",
@@ -44,11 +45,12 @@ _OCC_SEMANTICS = "o2"
 _DUCK_DTYPES = {torch.float32: _sdfr.F32, torch.float16: _sdfr.F16, torch.bfloat16: _sdfr.BF16,
                 torch.int32: _sdfr.I32, torch.int64: _sdfr.I64, torch.uint8: _sdfr.U8,
                 torch.bool: _sdfr.U8, torch.float64: _sdfr.F64}
-_GRID_DTYPES = {torch.float32: _sdfr.F32, torch.float16: _sdfr.F16}
+# voxel storage of the device copy: a torch dtype, or "r16" (4x4x4 bricks of
+# uint16 codes against a per-brick fp32 base and power-of-two scale)
+_GRID_DTYPES = {torch.float32: _sdfr.F32, torch.float16: _sdfr.F16, "r16": _sdfr.R16}
 _OUT_DTYPES = {torch.float32: _sdfr.F32, torch.bfloat16: _sdfr.BF16}
 _LAYOUTS = {"linear": _sdfr.LAYOUT_LINEAR, "brick4": _sdfr.LAYOUT_BRICK4}
-_SCHEDULES = {"persistent": _sdfr.SCHED_PERSISTENT, "tiles": _sdfr.SCHED_TILES,
-              "slots": _sdfr.SCHED_SLOTS}
+_SCHEDULES = {"persistent": _sdfr.SCHED_PERSISTENT, "tiles": _sdfr.SCHED_TILES}
 _TILE_ORDERS = {"launch": _sdfr.ORDER_LAUNCH, "lookahead": _sdfr.ORDER_LOOKAHEAD}
 
 
@@ -81,54 +83,132 @@ def _map_sig(bsp: Path) -> str:
     return f"v{_SDF_BUILDER_VERSION}_{st.st_size}_{st.st_mtime_ns}"
 
 
-def _load_occ_cache(core, cell, cache_dir, kind: str, semantics: str):
-    bsp = Path(core.bsp_path)
-    sig = f"{_map_sig(bsp)}_{semantics}"
-    cache = Path(cache_dir) if cache_dir else bsp.parent
-    f = cache / f"{bsp.stem}.{kind}_{cell:g}.npz"
-    if f.exists():
-        z = np.load(f, allow_pickle=False)
+def _cached(path: Path, sig: str, keys):
+    """The arrays `keys` of the cache file `path` if it exists and carries
+    signature `sig`, else None (the reference's cache test, vision.py:334-338)."""
+    if path.exists():
+        z = np.load(path, allow_pickle=False)
         if "sig" in z and str(z["sig"]) == sig:
-            return z["occ"], z["mins"].astype(np.float64)
-    raise FileNotFoundError(
-        f"no current occupancy cache at {f} (signature {sig}); sampling the map's occupancy "
-        "needs the reference's BSP core — sample it once with the reference")
+            return tuple(z[k] for k in keys)
+    return None
+
+
+def _cache_file(core, cell, cache_dir, kind: str) -> Path:
+    bsp = Path(core.bsp_path)
+    cache = Path(cache_dir) if cache_dir else bsp.parent
+    return cache / f"{bsp.stem}.{kind}_{cell:g}.npz"
+
+
+def _sibling(name: str):
+    """A module of the package this one is loaded in: the reference's own
+    ``surfgym.<name>`` when this module is installed into the reference's
+    package (surfgym_mi355x.install)."""
+    import importlib
+    try:
+        return importlib.import_module(f"{__package__}.{name}")
+    except ImportError as e:
+        raise ImportError(
+            f"{__package__}.{name} is needed to sample a map (it parses the BSP); install this "
+            "renderer into the reference's surfgym package (surfgym_mi355x.install) or bake "
+            "the map's caches with the reference") from e
 
 
 def map_occupancy(core, cell: float = 16.0, cache_dir=None):
     """The map's voxel-centre solid occupancy, (occ uint8 [nz, ny, nx],
-    mins float64 (3,)), from the reference's cache ``<map>.occ_<cell>.npz``
-    with its signature (vision.py:325-343)."""
-    return _load_occ_cache(core, cell, cache_dir, "occ", _OCC_SEMANTICS)
+    mins float64 (3,)), cached as ``<map>.occ_<cell>.npz`` (vision.py:325-343).
+    On a miss the map core samples it on grid_dims' voxels
+    (``core.occupancy_grid``, the C core's surf_occupancy_grid)."""
+    bsp = Path(core.bsp_path)
+    sig = f"{_map_sig(bsp)}_{_OCC_SEMANTICS}"
+    path = _cache_file(core, cell, cache_dir, "occ")
+    hit = _cached(path, sig, ("occ", "mins"))
+    if hit is not None:
+        return hit[0], hit[1].astype(np.float64)
+    mins, nx, ny, nz = grid_dims(core, cell)
+    occ = core.occupancy_grid(mins, cell, nx, ny, nz)
+    np.savez_compressed(path, occ=occ, mins=mins, sig=np.str_(sig))
+    return occ, mins
+
+
+# Thin solid brushes the slab occupancy rasterises exactly: a bounding box
+# whose smallest side is at most this many units (vision.py:392-395).
+_THIN_UNITS = 20.0
 
 
 def slab_occupancy(core, cell: float = 16.0, cache_dir=None):
-    """The slab-catching occupancy the goal graph uses, from the reference's
-    cache ``<map>.slabocc_<cell>.npz`` with its signature (vision.py:346-369)."""
-    return _load_occ_cache(core, cell, cache_dir, "slabocc", _SDF_SEMANTICS)
+    """Occupancy that thin solids cannot slip through, cached as
+    ``<map>.slabocc_<cell>.npz`` (vision.py:346-406): the voxel-centre
+    occupancy ORed with twelve samplings whose origin is shifted by
+    +-cell/4 and +-cell/2 along each axis, plus the bounding boxes of thin
+    solid brush entities (smallest side <= 20 u; not-solid conveyors
+    skipped) rasterised outright. On a miss the map core does the sampling
+    and the package's BSP parser (``zones.parse_bsp``) lists the entities."""
+    bsp = Path(core.bsp_path)
+    sig = f"{_map_sig(bsp)}_{_SDF_SEMANTICS}"
+    path = _cache_file(core, cell, cache_dir, "slabocc")
+    hit = _cached(path, sig, ("occ", "mins"))
+    if hit is not None:
+        return hit[0], hit[1].astype(np.float64)
+    base, mins = map_occupancy(core, cell, cache_dir)
+    occ = np.array(base, copy=True)
+    nz, ny, nx = occ.shape
+    quarter = cell / 4.0
+    for axis in range(3):
+        for k in (-2, -1, 1, 2):
+            shift = np.zeros(3)
+            shift[axis] = k * quarter
+            occ |= core.occupancy_grid(mins + shift, cell, nx, ny, nz)
+    entities, bboxes = _sibling("zones").parse_bsp(bsp)
+    dims = np.array([nx, ny, nz])
+    n_thin = 0
+    for ent in entities:
+        cls, model = ent.get("classname"), ent.get("model", "")
+        if cls not in SOLID_ENT_CLASSES or not model.startswith("*"):
+            continue
+        if cls == "func_conveyor" and int(float(ent.get("spawnflags", 0))) & 2:
+            continue   # a not-solid conveyor (the core's solid set skips it)
+        k = int(model[1:])
+        if k >= len(bboxes):
+            continue
+        lo_u, hi_u = (np.asarray(v, np.float64) for v in bboxes[k])
+        if float((hi_u - lo_u).min()) > _THIN_UNITS:
+            continue
+        lo = np.maximum(np.floor((lo_u - mins) / cell - 0.001), 0).astype(int)
+        hi = np.minimum(np.ceil((hi_u - mins) / cell + 0.001), dims).astype(int)
+        occ[lo[2]:hi[2], lo[1]:hi[1], lo[0]:hi[0]] = 1
+        n_thin += 1
+    if n_thin:
+        print(f"slab occupancy: rasterized {n_thin} thin solid entities")
+    np.savez_compressed(path, occ=occ, mins=mins, sig=np.str_(sig))
+    return occ, mins
 
 
-def build_sdf(core, cell: float = 16.0, cache_dir=None):
-    """Load the map's baked distance field: (sdf [nz,ny,nx], mins (3,), cell).
+def build_sdf(core, cell: float = 16.0, cache_dir=None, device=None):
+    """The map's distance field: (sdf [nz,ny,nx], mins (3,) f32, cell).
 
-    Reads the reference's cache file ``<map>.sdf_<cell>.npz`` (keys sdf, mins,
-    cell, sig) and honours its signature (vision.py:268-280, :420-426), so an
-    existing bake is used as-is. Baking a map from scratch (BSP occupancy
-    sampling through the C core plus an EDT, vision.py:428-438) is not part of
-    this renderer; construct with :meth:`GpuLidar.from_grid` for any other
-    grid. Tests replace this function on the module, as the reference's do.
+    Loads ``<map>.sdf_<cell>.npz`` (keys sdf, mins, cell, sig) when its
+    signature is current (vision.py:409-426), so a bake the reference wrote is
+    used as-is. Otherwise bakes it on the GPU (vision.py:428-439): the slab
+    occupancy, padded with one layer of solid, through the exact distance
+    transform of :func:`sdf_from_occupancy` (bit for bit the reference's scipy
+    call for power-of-two cells), stored f16 above 100 M voxels, else f32,
+    and writes the cache file in the reference's format. ``device``: the GPU
+    of the bake (default: the current one). Tests replace this function on
+    the module, as the reference's do.
     """
     bsp = Path(core.bsp_path)
     sig = f"{_map_sig(bsp)}_{_SDF_SEMANTICS}"
-    cache = Path(cache_dir) if cache_dir else bsp.parent
-    f = cache / f"{bsp.stem}.sdf_{cell:g}.npz"
-    if f.exists():
-        z = np.load(f, allow_pickle=False)
-        if "sig" in z and str(z["sig"]) == sig:
-            return z["sdf"], z["mins"], float(z["cell"])
-    raise FileNotFoundError(
-        f"no current SDF bake at {f} (signature {sig}); bake it once with the "
-        "reference's build_sdf, or pass a grid to GpuLidar.from_grid")
+    path = _cache_file(core, cell, cache_dir, "sdf")
+    hit = _cached(path, sig, ("sdf", "mins", "cell"))
+    if hit is not None:
+        return hit[0], hit[1], float(hit[2])
+    occ, mins = slab_occupancy(core, cell, cache_dir)
+    if device is None:
+        device = torch.device("cuda", torch.cuda.current_device())
+    sdf = sdf_from_occupancy(occ, cell, device=device).cpu().numpy()
+    mins32 = np.asarray(mins).astype(np.float32)
+    np.savez_compressed(path, sdf=sdf, mins=mins32, cell=np.float32(cell), sig=np.str_(sig))
+    return sdf, mins32, cell
 
 
 @torch.no_grad()
@@ -196,7 +276,10 @@ class GpuLidar:
     Keyword-only extensions (defaults reproduce the reference):
 
     * ``grid_dtype`` — voxel storage, torch.float16 as the reference stores
-      it (vision.py:476-477) or torch.float32;
+      it (vision.py:476-477), torch.float32, or ``"r16"``: 4x4x4 bricks of
+      uint16 codes against a per-brick fp32 base and power-of-two scale,
+      two bytes per voxel like fp16 but within scale/2 of the fp32 grid
+      (2^-10 u at 16 u cells) at any distance;
     * ``layout`` — the device copy's order, "brick4" (4x4x4 bricks) or
       "linear";
     * ``hit_eps`` / ``min_step`` — the step rule's constants, 0.6*cell and
@@ -205,11 +288,9 @@ class GpuLidar:
       schedules rays: launch-scheduled waves of 8x8 pixel "tiles", each lane
       marching ``rays_per_lane`` rays at once (default None: each render
       picks 1 for grids above 192 MiB and for renders under 512 envs of
-      128x64, else 2; see :meth:`effective_rays_per_lane`); "slots",
-      persistent waves holding
-      ``rays_per_lane`` (1-4) tiles that each take a new tile when their 64
-      rays end; or "persistent" waves that refill lanes with new rays once
-      ``refill_lanes`` of them have finished. The results are identical;
+      128x64, else 2; see :meth:`effective_rays_per_lane`); or "persistent"
+      waves that refill lanes with new rays once ``refill_lanes`` of them
+      have finished. The results are identical;
     * ``tile_order`` — "lookahead" (default) or "launch": see
       :meth:`set_tile_order`.
     """
@@ -227,8 +308,8 @@ class GpuLidar:
                  _surf_nz=None) -> None:
         if surf_mask and pinhole:
             raise ValueError(
-                "surf_mask and pinhole are separate experiments and there is "
-                "no combined kernel")
+                "pinhole=True with surf_mask=True: the surf-mask channel is rendered for the "
+                "equiangular camera only; there is no combined kernel")
         self.device = torch.device(device)
         if self.device.type != "cuda":
             raise ValueError(f"GpuLidar renders on a ROCm GPU (device='cuda'), got {device!r}; "
@@ -236,7 +317,10 @@ class GpuLidar:
         if self.device.index is None:
             self.device = torch.device("cuda", torch.cuda.current_device())
         if grid_dtype not in _GRID_DTYPES:
-            raise ValueError(f"grid_dtype must be torch.float16 or torch.float32, got {grid_dtype}")
+            raise ValueError(f"grid_dtype must be torch.float16, torch.float32 or 'r16', "
+                             f"got {grid_dtype!r}")
+        if grid_dtype == "r16" and layout != "brick4":
+            raise ValueError("the r16 store exists in the brick4 layout only")
         if layout not in _LAYOUTS:
             raise ValueError(f"layout must be one of {sorted(_LAYOUTS)}, got {layout!r}")
         if schedule not in _SCHEDULES:
@@ -246,8 +330,10 @@ class GpuLidar:
         sdf = np.asarray(sdf)
         if sdf.ndim != 3:
             raise ValueError(f"the grid must be [nz, ny, nx], got shape {sdf.shape}")
-        # flat grid + integer strides, the reference's attributes (vision.py:476-480)
-        self.sdf_flat = torch.as_tensor(sdf, device=self.device).to(grid_dtype).reshape(-1)
+        # flat grid + integer strides, the reference's attributes (vision.py:476-480);
+        # an r16 copy is encoded from the fp32 values
+        flat_dtype = torch.float32 if grid_dtype == "r16" else grid_dtype
+        self.sdf_flat = torch.as_tensor(sdf, device=self.device).to(flat_dtype).reshape(-1)
         self.nz, self.ny, self.nx = (int(v) for v in sdf.shape)
         self.stride_z = self.ny * self.nx
         self.stride_y = self.nx
@@ -269,8 +355,8 @@ class GpuLidar:
                 snz = np.asarray(snz)
             if snz.shape != sdf.shape:
                 raise RuntimeError(
-                    f"surfability grid {snz.shape} != SDF grid {sdf.shape}: "
-                    "the march reads both with ONE voxel index")
+                    f"surf-mask grid {snz.shape} does not match the distance grid {sdf.shape}; "
+                    "a single voxel index addresses both")
             self.snz_flat = torch.as_tensor(snz.astype(np.int8, copy=False),
                                             device=self.device).reshape(-1)
         self.W, self.H = int(width), int(height)
@@ -308,11 +394,12 @@ class GpuLidar:
         with torch.cuda.device(self.device):
             stream = torch.cuda.current_stream(self.device)
             h = self._lib.sdfr_grid_create(ctypes.byref(desc), self.sdf_flat.data_ptr(),
-                                           _GRID_DTYPES[grid_dtype], 1, _GRID_DTYPES[grid_dtype],
+                                           _GRID_DTYPES[flat_dtype], 1, _GRID_DTYPES[grid_dtype],
                                            _LAYOUTS[layout], stream.cuda_stream, err, len(err))
         if not h:
             raise _sdfr.SdfrError(err.value.decode("utf-8", "replace"))
         self._grid = h
+        self._ws_retired = []   # workspaces captured renders still point at
         if self.surf_mask:
             with torch.cuda.device(self.device):
                 stream = torch.cuda.current_stream(self.device).cuda_stream
@@ -337,8 +424,8 @@ class GpuLidar:
         self.rays_per_lane = None if rays_per_lane is None else rpl
 
     def effective_rays_per_lane(self, n_envs: int) -> int:
-        """Rays per lane (tiles schedule) or slots per wave (slots schedule)
-        a render of ``n_envs`` images runs with."""
+        """Rays per lane a render of ``n_envs`` images runs with (tiles
+        schedule and surf-mask renders)."""
         r = int(self._lib.sdfr_render_rays_per_lane(self._grid, ctypes.byref(self._cam()),
                                                     int(n_envs)))
         if r < 0:
@@ -394,7 +481,9 @@ class GpuLidar:
     def _workspace(self, cam, n: int) -> torch.Tensor:
         """The render's ray-table scratch, kept and grown with N. It is
         allocated outside the render call, so a render captured into a graph
-        after one eager render of the same N allocates nothing."""
+        after one eager render of the same N allocates nothing. A buffer that
+        a captured render has used stays alive for the lidar's lifetime when
+        a larger render replaces it: the graph replays write to its address."""
         need = self._ws_need.get(n)
         if need is None:
             need = int(self._lib.sdfr_workspace_bytes(ctypes.byref(cam), n))
@@ -403,8 +492,13 @@ class GpuLidar:
             self._ws_need[n] = need
         ws = getattr(self, "_ws", None)
         if ws is None or ws.numel() < need:
+            if ws is not None and getattr(self, "_ws_captured", False):
+                self._ws_retired.append(ws)
             ws = torch.empty(need, dtype=torch.uint8, device=self.device)
             self._ws = ws
+            self._ws_captured = False
+        if not self._ws_captured and torch.cuda.is_current_stream_capturing():
+            self._ws_captured = True
         return ws
 
     def _cam(self) -> _sdfr.Cam:
@@ -581,6 +675,17 @@ class GpuLidar:
     def _dirs_pinhole(self, N, yaw_deg, pitch_deg, d2r):
         """Tangent-plane directions into ``_dx/_dy/_dz`` (vision.py:609-624)."""
         self._dirs_into(N, yaw_deg, pitch_deg, d2r, True)
+
+    @torch.no_grad()
+    def stored_grid(self) -> torch.Tensor:
+        """The device copy the march samples, read back as [nz, ny, nx]
+        float32 (fp16 widened, r16 decoded)."""
+        out = torch.empty(self.nz, self.ny, self.nx, device=self.device)
+        with torch.cuda.device(self.device):
+            rc = self._lib.sdfr_grid_read(self._grid, out.data_ptr(),
+                                          torch.cuda.current_stream(self.device).cuda_stream)
+        _sdfr.check(rc, "sdfr_grid_read", self._lib)
+        return out
 
     @property
     def grid_bytes(self) -> int:

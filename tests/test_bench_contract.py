@@ -22,26 +22,61 @@ def test_more_than_one_gpu_is_refused_with_a_message():
     assert "one GPU" in (r.stdout + r.stderr) or "single MI355X" in (r.stdout + r.stderr)
 
 
-def test_every_traffic_line_in_profiles_parses_and_is_found():
-    lines = []
+def test_every_profile_record_parses_and_names_its_kernels():
+    """Each traffic_bytes_per_launch / limiter line under profiles/ parses,
+    is found by the lookup bench.py uses, and sits in a file that records
+    the hash of the kernels' source it was measured on."""
+    traffic, limiter = bench.profile_records()
+    assert traffic and limiter
+    seen = []
     for f in sorted((ROOT / "profiles").glob("*.md")):
-        for line in f.read_text().splitlines():
-            if line.strip().startswith("traffic_bytes_per_launch["):
-                m = re.match(r"traffic_bytes_per_launch\[(.+?)\] = (\d+)$", line.strip())
-                assert m, (f.name, line)
-                lines.append((m.group(1), int(m.group(2))))
-    keys = [k for k, _ in lines]
-    assert len(keys) == len(set(keys)), "a configuration is profiled twice"
-    for k, v in lines:
-        assert bench.profiled_traffic(k) == v
-    # the default workload's key, as bench.py builds it
-    assert bench.profiled_traffic("ramp_field tiles rpl=2 brick4 f32 order=lookahead")
-    assert bench.profiled_traffic("no such workload") is None
+        text = f.read_text()
+        keys = re.findall(r"^traffic_bytes_per_launch\[(.+?)\] = \d+$", text, re.M)
+        keys += re.findall(r"^limiter\[(.+?)\] = \{", text, re.M)
+        if keys:
+            assert re.search(r"^sdfr_hip_sha256 = [0-9a-f]{64}$", text, re.M), f.name
+        seen += keys
+    for k, rec in traffic.items():
+        assert rec["bytes"] > 0 and rec["profile"].startswith("profiles/"), k
+    for k, rec in limiter.items():
+        assert 0.0 < rec["busy"] <= 1.0 and rec["unit"], k
+    assert bench.profiled("no such workload", traffic, "bytes") == (None, None)
+
+
+def test_profiles_were_measured_on_the_current_kernels():
+    """A change to csrc/sdfr.hip makes every profiled figure stale: re-profile
+    (the commands are in each summary) and record the new hash."""
+    traffic, limiter = bench.profile_records()
+    now = bench.sdfr_source_sha256()
+    stale = sorted({rec["profile"] for rec in list(traffic.values()) + list(limiter.values())
+                    if rec["sdfr_hip_sha256"] != now})
+    assert not stale, f"profiled on other kernels than csrc/sdfr.hip now holds: {stale}"
 
 
 @pytest.mark.parametrize("key", ["ramp_field tiles rpl=2 brick4 f32 order=lookahead",
                                  "winding_track tiles rpl=1 brick4 f32 order=lookahead",
                                  "sparse_grazing tiles rpl=2 brick4 f32 order=lookahead",
-                                 "ramp_field_f16_bf16 tiles rpl=2 brick4 f16 order=lookahead"])
+                                 "ramp_field_r16_bf16 tiles rpl=2 brick4 r16 order=lookahead"])
 def test_bench_workloads_have_profiled_traffic(key):
-    assert bench.profiled_traffic(key) > 0
+    traffic, _ = bench.profile_records()
+    value, src = bench.profiled(key, traffic, "bytes")
+    assert src is not None and src["current"], key
+    assert value > 0
+
+
+@pytest.mark.parametrize("name", ["ramp_field", "winding_track", "sparse_grazing",
+                                  "ramp_field_r16_bf16", "small_ramps"])
+def test_bench_workloads_have_a_measured_limiter(name):
+    _, limiter = bench.profile_records()
+    value, src = bench.profiled(name, limiter)
+    assert src is not None and src["current"], name
+    assert value["unit"] and 0.0 < value["busy"] <= 1.0
+
+
+def test_other_configurations_cover_the_metric_workloads():
+    names = {n for n, _, _ in bench.OTHER_CONFIGS}
+    assert names == {"small_ramps", "winding_track", "sparse_grazing", "ramp_field_r16_bf16"}
+    graph = {n: g for n, g, _ in bench.OTHER_CONFIGS}
+    assert graph["ramp_field_r16_bf16"] is True
+    shape = {n: s for n, _, s in bench.OTHER_CONFIGS}["ramp_field_r16_bf16"]
+    assert shape(8192) == (8192, 1, 64, 128)

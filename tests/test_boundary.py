@@ -88,6 +88,9 @@ def test_grid_create_rejects_bad_descriptors_without_a_device():
         (_sdfr.GridDesc(2, 2, 2, (ctypes.c_float * 3)(), 16.0), 42, 0, 0, "source dtype"),
         (_sdfr.GridDesc(2, 2, 2, (ctypes.c_float * 3)(), 16.0), 0, 2, 0, "store dtype"),
         (_sdfr.GridDesc(2, 2, 2, (ctypes.c_float * 3)(), 16.0), 0, 0, 9, "layout"),
+        (_sdfr.GridDesc(2, 2, 2, (ctypes.c_float * 3)(), 16.0), 0, _sdfr.R16,
+         _sdfr.LAYOUT_LINEAR, "brick4 layout only"),
+        (_sdfr.GridDesc(2, 2, 2, (ctypes.c_float * 3)(), 16.0), 0, 9, 1, "store dtype"),
     ]:
         h = lib.sdfr_grid_create(ctypes.byref(desc), src.ctypes.data, dtype, 0, store, layout,
                                  None, err, len(err))
@@ -100,6 +103,9 @@ def test_grid_create_rejects_bad_descriptors_without_a_device():
 def test_schedule_and_tile_order_reject_a_null_handle_without_a_device():
     from surfgym import _sdfr
     lib = _sdfr.load()
+    assert lib.sdfr_grid_read(None, None, None) == -1
+    assert "null grid" in _sdfr.last_error()
+    assert lib.sdfr_grid_set_schedule(None, 2, 16, 0) == -1      # no slot schedule any more
     assert lib.sdfr_grid_set_tile_order(None, _sdfr.ORDER_LOOKAHEAD, -1) == -1
     assert "null grid" in _sdfr.last_error()
     assert lib.sdfr_grid_set_schedule(None, _sdfr.SCHED_TILES, 16, 2) == -1
@@ -247,17 +253,6 @@ def test_goal_seed_box_and_cache_contract(tmp_path):
     assert sig == f"g4_v2_{st.st_size}_{st.st_mtime_ns}_1_-2_3_10_20_30.6"
     assert goalfield._goal_sig(bsp, zone, True).startswith("g4_k1_v2_")
 
-    class Core:
-        bsp_path = str(bsp)
-
-    with pytest.raises(FileNotFoundError, match="slabocc"):
-        goalfield.build_goal_field(Core(), zone, 16.0)
-    with pytest.raises(NotImplementedError):
-        goalfield.build_goal_field(Core(), zone, 16.0, mask_kill=True)
-    np.savez(tmp_path / "surf_x.slabocc_16.npz", occ=np.zeros((2, 2, 2), np.uint8),
-             mins=np.zeros(3), sig=np.str_("stale"))
-    with pytest.raises(FileNotFoundError, match="no current occupancy cache"):
-        goalfield.build_goal_field(Core(), zone, 16.0)
     with pytest.raises(ValueError, match="no CPU path"):
         goalfield.GoalField(np.zeros((2, 2, 2), np.float32), np.zeros(3), 16.0, 10.0,
                             device="cpu")
@@ -266,29 +261,3 @@ def test_goal_seed_box_and_cache_contract(tmp_path):
                                             device="cpu")
 
 
-def test_occupancy_caches_load_under_the_reference_signatures(tmp_path):
-    """map_occupancy / slab_occupancy read the reference's cache files
-    (vision.py:325-369): current signature -> the arrays, otherwise an error
-    (sampling needs the BSP core)."""
-    from surfgym import vision
-    bsp = tmp_path / "surf_y.bsp"
-    bsp.write_bytes(b"x" * 123)
-    st = bsp.stat()
-
-    class Core:
-        bsp_path = str(bsp)
-
-    occ = (np.arange(24).reshape(2, 3, 4) % 3 == 0).astype(np.uint8)
-    for kind, fn, sem in (("occ", vision.map_occupancy, "o2"),
-                          ("slabocc", vision.slab_occupancy, "s4")):
-        f = tmp_path / f"surf_y.{kind}_32.npz"
-        with pytest.raises(FileNotFoundError):
-            fn(Core(), 32.0)
-        np.savez_compressed(f, occ=occ, mins=np.array([1.0, 2.0, 3.0], np.float32),
-                            sig=np.str_(f"v2_{st.st_size}_{st.st_mtime_ns}_{sem}"))
-        got, mins = fn(Core(), 32.0)
-        assert np.array_equal(got, occ) and mins.dtype == np.float64
-        assert mins.tolist() == [1.0, 2.0, 3.0]
-        np.savez_compressed(f, occ=occ, mins=np.zeros(3), sig=np.str_("v2_0_0_" + sem))
-        with pytest.raises(FileNotFoundError):
-            fn(Core(), 32.0)

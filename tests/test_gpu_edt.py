@@ -53,3 +53,34 @@ def test_scene_occupancy_matches_scipy_and_renders(dev):
     img = lid.render(torch.as_tensor(ps.origin, device=dev), torch.as_tensor(ps.yaw, device=dev),
                      torch.as_tensor(ps.pitch, device=dev), torch.as_tensor(ps.ducked, device=dev))
     assert torch.isfinite(img).all() and img.min() >= 0
+
+
+def test_build_sdf_bakes_a_map_on_the_gpu_and_caches_it(dev, tmp_path, monkeypatch):
+    """build_sdf on a map without a cache (vision.py:409-439): the slab
+    occupancy, sampled through the map core, baked on the GPU; the npz it
+    writes equals the reference's scipy bake of that occupancy bit for bit,
+    and a second call loads it without baking."""
+    import sys
+    from test_drop_in import _Core, _zones_module
+    bsp = tmp_path / "surf_g.bsp"
+    bsp.write_bytes(b"BSP" * 50)
+    core = _Core(bsp, [((0, 0, 0), (512, 384, 40)), ((100, 50, 40), (300, 90, 140)),
+                       ((0, 0, 200), (512, 384, 203))], ((0, 0, 0), (512, 384, 256)))
+    monkeypatch.setitem(sys.modules, "surfgym.zones", _zones_module(
+        [{"classname": "func_wall", "model": "*1"}], [None, ((400.0, 0.0, 0.0),
+                                                             (401.0, 300.0, 120.0))]))
+    print("case build_sdf GPU bake", flush=True)
+    sdf, mins, cell = vision.build_sdf(core, 16.0, device=dev)
+    occ, omins = vision.slab_occupancy(core, 16.0)
+    want = edt.stored(edt.bake(occ, 16.0))
+    assert sdf.dtype == want.dtype and np.array_equal(sdf, want)
+    z = np.load(tmp_path / "surf_g.sdf_16.npz", allow_pickle=False)
+    assert np.array_equal(z["sdf"], want) and np.array_equal(z["mins"], omins.astype(np.float32))
+    assert float(z["cell"]) == 16.0
+
+    def no_bake(*a, **k):
+        raise AssertionError("a current cache must not be baked again")
+
+    monkeypatch.setattr(vision, "sdf_from_occupancy", no_bake)
+    again, _, _ = vision.build_sdf(core, 16.0, device=dev)
+    assert np.array_equal(again, want)

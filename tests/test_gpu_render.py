@@ -315,8 +315,7 @@ def test_step_rule_corners_are_exact_in_every_schedule(dev, max_steps, hit_eps, 
         lid = vision.GpuLidar.from_grid(sc.sdf, sc.mins, sc.cell, width=w.width,
                                         height=w.height, grid_dtype=gdt, device=dev, **kw)
         for sched, rpl, order in (("tiles", 2, "lookahead"), ("tiles", 2, "launch"),
-                                  ("tiles", 1, "lookahead"), ("slots", 2, "launch"),
-                                  ("persistent", None, "launch")):
+                                  ("tiles", 1, "lookahead"), ("persistent", None, "launch")):
             lid.set_schedule(sched, rays_per_lane=rpl)
             lid.set_tile_order(order, min_tiles=0)
             taps = torch.full((n, w.height, w.width), -1, dtype=torch.int32, device=dev)
@@ -361,70 +360,6 @@ def test_schedules_give_identical_results(dev, refill, rpl):
     assert torch.equal(ta, tb)
 
 
-@pytest.mark.parametrize("slots", [1, 2, 3, 4])
-def test_slots_schedule_gives_identical_results(dev, slots):
-    """Persistent waves of R tile slots march the same rays as the tiles
-    schedule: outputs and censuses bit-identical, for every R."""
-    w, sc = _scene("ramp_field")
-    ps = w.poses(sc, 96)
-    _say(f"case slots R={slots}")
-    lid = _lidar(dev, w, sc)
-    n = len(ps)
-    lid.set_schedule("tiles")
-    ta = torch.empty(n, w.height, w.width, dtype=torch.int32, device=dev)
-    a = _gpu_render(lid, ps, dev, taps=ta)
-    lid.set_schedule("slots", rays_per_lane=slots)
-    tb = torch.empty_like(ta)
-    b = _gpu_render(lid, ps, dev, taps=tb)
-    assert torch.equal(a, b)
-    assert torch.equal(ta, tb)
-
-
-@pytest.mark.parametrize("W,H,n", [(8, 8, 1), (9, 7, 3), (128, 64, 1), (40, 24, 5)])
-def test_slots_schedule_covers_small_and_ragged_batches(dev, W, H, n):
-    """Fewer tiles than XCD partitions, partial tiles: every pixel written."""
-    w, sc = _scene("small_ramps")
-    ps = w.poses(sc, n)
-    _say(f"case slots ragged W={W} H={H} n={n}")
-    lid = vision.GpuLidar.from_grid(sc.sdf, sc.mins, sc.cell, width=W, height=H,
-                                    range_units=w.range_units, near_range=w.near_range,
-                                    max_steps=w.max_steps, hit_eps=w.hit_eps,
-                                    grid_dtype=torch.float32, schedule="slots", rays_per_lane=4,
-                                    device=dev)
-    out = torch.full((n, H, W), -1.0, device=dev)
-    _gpu_render(lid, ps, dev, out=out)
-    want, _ = _oracle(w, sc, ps, width=W, height=H)
-    assert np.array_equal(out.cpu().numpy(), want)
-
-
-def test_slots_schedule_replays_in_a_graph(dev):
-    w, sc = _scene("small_ramps")
-    ps = w.poses(sc)
-    _say("case slots graph")
-    lid = _lidar(dev, w, sc, schedule="slots", rays_per_lane=2)
-    origin = torch.as_tensor(ps.origin, device=dev)
-    yaw = torch.as_tensor(ps.yaw, device=dev)
-    pitch = torch.as_tensor(ps.pitch, device=dev)
-    duck = torch.as_tensor(ps.ducked, device=dev)
-    want = lid.render(origin, yaw, pitch, duck).clone()
-    out = torch.empty_like(want)
-    s = torch.cuda.Stream(device=dev)
-    s.wait_stream(torch.cuda.current_stream(dev))
-    with torch.cuda.stream(s):
-        lid.render(origin, yaw, pitch, duck, out=out)
-    torch.cuda.current_stream(dev).wait_stream(s)
-    torch.cuda.synchronize()
-    g = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(g):
-        lid.render(origin, yaw, pitch, duck, out=out)
-    for i in range(3):
-        out.fill_(-1.0)
-        g.replay()
-        torch.cuda.synchronize()
-        assert torch.equal(out, want), i
-        assert torch.equal(lid.render(origin, yaw, pitch, duck), want)
-
-
 def test_schedule_arguments_are_checked(dev):
     from surfgym import _sdfr
     w, sc = _scene("small_ramps")
@@ -439,14 +374,14 @@ def test_schedule_arguments_are_checked(dev):
         lid.set_schedule("tiles", rays_per_lane=3)
     with pytest.raises(_sdfr.SdfrError, match="rays_per_lane"):
         lid.set_schedule("tiles", rays_per_lane=-1)
-    with pytest.raises(_sdfr.SdfrError, match="rays_per_lane"):
-        lid.set_schedule("slots", rays_per_lane=5)
     with pytest.raises(_sdfr.SdfrError, match="refill_lanes"):
         lid.set_schedule("persistent", refill_lanes=0)
     with pytest.raises(ValueError, match="schedule"):
         lid.set_schedule("bogus")
-    lid.set_schedule("slots", rays_per_lane=4)
-    assert (lid.schedule, lid.rays_per_lane) == ("slots", 4)
+    with pytest.raises(ValueError, match="schedule"):
+        lid.set_schedule("slots")      # the slot schedule measured slower and is gone
+    lid.set_schedule("persistent", refill_lanes=8, rays_per_lane=2)
+    assert (lid.schedule, lid.rays_per_lane) == ("persistent", 2)
 
 
 @pytest.mark.parametrize("name,n,rpl", [("ramp_field", 256, None), ("ramp_field", 256, 2),
@@ -631,7 +566,7 @@ def test_sparse_grazing_matches_the_oracle(dev):
     ps = w.poses(sc, 256)
     _say(f"case sparse_grazing envs={len(ps)}")
     lid = _lidar(dev, w, sc)
-    for sched in ("tiles", "persistent", "slots"):
+    for sched in ("tiles", "persistent"):
         lid.set_schedule(sched)
         got = _gpu_render(lid, ps, dev).cpu().numpy()
         want, _ = _oracle(w, sc, ps)

@@ -1,10 +1,13 @@
 """The surf-mask channel (GpuLidar(surf_mask=True), reference
 python/surfgym/vision.py:118-191, 558-570, 658-666) on the GPU.
 
-The first three tests restate the reference's renderer tests of the mask
-(tests/python/test_surfmask.py:174-240) — a floor-slab world with an
-analytic SDF — against this renderer; the last compares both channels with
-the CPU oracle ray for ray.
+The reference checks its mask renderer on an analytic world
+(tests/python/test_surfmask.py:174-240): the channel must not disturb the
+depth, must report the |n_z| of the voxel a ray stops in (1 on a flat floor,
+0 where a ray runs out into the sky), and must come out interleaved with the
+depth, channel fastest. The same three properties are checked here on a
+terrace world of this file's own, then both channels against the CPU
+oracle ray for ray, in every schedule.
 """
 from __future__ import annotations
 
@@ -17,71 +20,110 @@ from surfgym import synth, vision
 
 pytestmark = pytest.mark.gpu
 
-RCELL = 16.0
-RNX, RNY, RNZ = 32, 32, 16
+CELL = 16.0
+NX, NY, NZ = 40, 24, 20
+SLOPE_X = 20          # columns ix >= SLOPE_X carry a sloped surface's |n_z|
+SLOPE_NZ = 90         # |n_z| * 127 of that surface (about 45 degrees)
 
 
-def _floor_world():
-    sdf = (np.arange(RNZ, dtype=np.float32) * RCELL)[:, None, None] \
-        * np.ones((1, RNY, RNX), dtype=np.float32)
-    snz = np.zeros((RNZ, RNY, RNX), dtype=np.int8)
-    snz[0] = 127                                        # the floor is flat
+def _terrace():
+    """Ground below z = 0: each voxel's distance is its centre height, the
+    bottom layer is the surface, flat (127) west of SLOPE_X and tilted
+    (SLOPE_NZ) east of it; every voxel above the bottom layer reads 0."""
+    sdf = np.broadcast_to(((np.arange(NZ) + 0.5) * CELL).astype(np.float32)[:, None, None],
+                          (NZ, NY, NX)).copy()
+    sdf[0] = 0.0
+    snz = np.zeros((NZ, NY, NX), np.int8)
+    snz[0, :, :SLOPE_X] = 127
+    snz[0, :, SLOPE_X:] = SLOPE_NZ
     return sdf, snz
 
 
-def _poses(dev):
-    #                x      y      z (eye = z + 17)  yaw  pitch duck
-    a = np.array([[200.0, 200.0, 183.0, 0.0, -90.0, 0],    # straight down
-                  [200.0, 200.0, 183.0, 0.0, 80.0, 0],     # up into the sky
-                  [200.0, 200.0, 183.0, 45.0, -30.0, 0]], dtype=np.float32)
-    return (torch.as_tensor(a[:, 0:3], device=dev), torch.as_tensor(a[:, 3], device=dev),
-            torch.as_tensor(a[:, 4], device=dev), torch.as_tensor(a[:, 5], device=dev))
+# eye = origin + 17; (x, y, z, yaw, pitch, ducked)
+_VIEWS = np.array([[120.0, 190.0, 133.0, 0.0, -90.0, 0.0],     # down onto the flat part
+                   [520.0, 190.0, 128.0, 0.0, -90.0, 1.0],     # down onto the slope, ducked
+                   [300.0, 190.0, 133.0, 90.0, 65.0, 0.0]],    # up, out of the grid
+                  np.float32)
 
 
-def test_flag_off_changes_nothing(dev):
-    print("case surf-mask flag off", flush=True)
-    sdf, snz = _floor_world()
-    off = vision.GpuLidar.from_grid(sdf, np.zeros(3), RCELL, width=8, height=4, device=dev)
-    on = vision.GpuLidar.from_grid(sdf, np.zeros(3), RCELL, width=8, height=4, device=dev,
-                                   surf_nz=snz)
-    tensors = {k for k, v in vars(off).items() if torch.is_tensor(v)}
-    assert tensors == {"sdf_flat", "mins", "yoff", "poff"}
-    assert {k for k, v in vars(on).items() if torch.is_tensor(v)} - tensors == {"snz_flat"}
-    assert (off.surf_mask, off.channels) == (False, 1)
-    assert (on.surf_mask, on.channels) == (True, 2)
-    d = off.render(*_poses(dev))
-    both = on.render(*_poses(dev))
-    assert d.shape == (3, 4, 8) and both.shape == (3, 4, 8, 2)
-    assert torch.equal(both[..., 0], d), "the mask perturbed the depth channel"
+def _views(dev):
+    v = torch.as_tensor(_VIEWS, device=dev)
+    return v[:, 0:3], v[:, 3], v[:, 4], v[:, 5]
 
 
-def test_mask_channel_reads_the_hit_surface(dev):
-    print("case surf-mask reads the surface", flush=True)
-    sdf, snz = _floor_world()
-    lid = vision.GpuLidar.from_grid(sdf, np.zeros(3), RCELL, width=8, height=4, device=dev,
-                                    surf_nz=snz)
-    out = lid.render(*_poses(dev))
-    down, up = out[0], out[1]
-    assert down[..., 0].max() < 0.2, "the floor should be close below"
-    assert torch.all(down[..., 1] == 1.0), "flat floor must read |n_z| = 1"
-    assert torch.all(up[..., 0] > 0.9), "the sky pixels should run to range"
-    assert torch.all(up[..., 1] == 0.0), "open sky must read 0"
+def _lidar(dev, snz=None, **kw):
+    sdf, _ = _terrace()
+    return vision.GpuLidar.from_grid(sdf, np.zeros(3), CELL, width=12, height=6,
+                                     range_units=1200.0, surf_nz=snz, device=dev, **kw)
 
 
-def test_flat_image_is_channel_fastest(dev):
-    print("case surf-mask layout", flush=True)
-    sdf, snz = _floor_world()
-    lid = vision.GpuLidar.from_grid(sdf, np.zeros(3), RCELL, width=8, height=4, device=dev,
-                                    surf_nz=snz)
-    out = lid.render(*_poses(dev))
+def test_the_mask_channel_leaves_the_depth_channel_alone(dev):
+    print("case surf-mask: depth channel unchanged", flush=True)
+    _, snz = _terrace()
+    plain, masked = _lidar(dev), _lidar(dev, snz)
+    assert (plain.surf_mask, plain.channels) == (False, 1)
+    assert (masked.surf_mask, masked.channels) == (True, 2)
+    base = {k for k, v in vars(plain).items() if torch.is_tensor(v)}
+    extra = {k for k, v in vars(masked).items() if torch.is_tensor(v)} - base
+    assert extra == {"snz_flat"}, extra
+    d = plain.render(*_views(dev))
+    both = masked.render(*_views(dev))
+    assert d.shape == (3, 6, 12) and both.shape == (3, 6, 12, 2)
+    assert torch.equal(both[..., 0], d)
+
+
+def test_the_mask_channel_reports_the_surface_under_the_hit(dev):
+    print("case surf-mask: surface under the hit", flush=True)
+    _, snz = _terrace()
+    out = _lidar(dev, snz).render(*_views(dev)).cpu()
+    flat, slope, sky = out[0], out[1], out[2]
+    assert float(flat[..., 0].max()) < 0.2 and float(slope[..., 0].max()) < 0.2
+    assert torch.all(flat[..., 1] == 1.0)
+    assert torch.all(slope[..., 1] == torch.tensor(SLOPE_NZ / 127.0))
+    assert torch.all(sky[..., 0] == 1.0)          # ran to range, encoding clamps at 1
+    assert torch.all(sky[..., 1] == 0.0)
+
+
+def test_the_two_channels_are_interleaved(dev):
+    print("case surf-mask: interleaved layout", flush=True)
+    _, snz = _terrace()
+    lid = _lidar(dev, snz)
+    out = lid.render(*_views(dev))
+    assert out.is_contiguous() and out.stride()[-1] == 1 and out.shape[-1] == 2
     flat = out.reshape(3, -1)
-    assert torch.equal(flat.reshape(-1, 4, 8, 2), out)
-    im = flat.reshape(-1, 4, 8, 2).permute(0, 3, 1, 2)
-    assert im.stride()[1] == 1, "channel stride must be 1 (NHWC)"
-    # and it can be written straight into an observation row
-    obs = torch.full((3, 15 + 4 * 8 * 2), -3.0, device=dev)
-    lid.render(*_poses(dev), out=obs[:, 15:])
-    assert torch.equal(obs[:, 15:], flat) and torch.all(obs[:, :15] == -3.0)
+    assert torch.equal(flat[:, 0::2].reshape(3, 6, 12), out[..., 0])
+    assert torch.equal(flat[:, 1::2].reshape(3, 6, 12), out[..., 1])
+    row = torch.full((3, 15 + flat.shape[1] + 4), -3.0, device=dev)
+    lid.render(*_views(dev), out=row[:, 15:15 + flat.shape[1]])
+    assert torch.equal(row[:, 15:15 + flat.shape[1]], flat)
+    assert torch.all(row[:, :15] == -3.0) and torch.all(row[:, -4:] == -3.0)
+
+
+@pytest.mark.parametrize("schedule,rpl", [("persistent", None), ("persistent", 2),
+                                          ("tiles", 1), ("tiles", 2)])
+def test_every_pixel_is_written_whatever_the_schedule(dev, schedule, rpl):
+    """The mask renders with the tiles kernel whatever schedule the handle is
+    set to; every pixel of a -1-filled output is written and equals the
+    oracle's, sorted or not."""
+    w = synth.WORKLOADS["small_ramps"]
+    sc = w.scene()
+    ps = w.poses(sc)
+    snz = np.random.default_rng(3).integers(0, 128, sc.sdf.shape).astype(np.int8)
+    print(f"case surf-mask schedule={schedule} rpl={rpl}", flush=True)
+    lid = vision.GpuLidar.from_grid(sc.sdf, sc.mins, sc.cell, surf_nz=snz,
+                                    range_units=w.range_units, near_range=w.near_range,
+                                    max_steps=w.max_steps, hit_eps=w.hit_eps,
+                                    grid_dtype=torch.float32, schedule=schedule,
+                                    rays_per_lane=rpl, device=dev)
+    want, _ = oracle.render(sc.sdf, sc.mins, sc.cell, ps.origin, ps.yaw, ps.pitch, ps.ducked,
+                            range_units=w.range_units, near_range=w.near_range,
+                            hit_eps=w.hit_eps, max_steps=w.max_steps, surf_nz=snz, threads=16)
+    args = [torch.as_tensor(v, device=dev) for v in (ps.origin, ps.yaw, ps.pitch, ps.ducked)]
+    for min_tiles in (0, None):
+        lid.set_tile_order("lookahead", min_tiles=min_tiles)
+        out = torch.full((len(ps), w.height, w.width, 2), -1.0, device=dev)
+        lid.render(*args, out=out)
+        assert np.array_equal(out.cpu().numpy(), want), min_tiles
 
 
 @pytest.mark.parametrize("layout,out_dtype,rpl", [("brick4", torch.float32, None),
