@@ -221,6 +221,24 @@ SDFR_API int32_t sdfr_render(const SdfrGrid* grid, const SdfrCam* cam,
                              const SdfrPoses* poses, const SdfrImage* image,
                              void* workspace, int64_t workspace_size, void* stream);
 
+/* Size of the device array sdfr_render_noalloc uses as its workspace: the
+ * sdfr_workspace_bytes() of 8192 envs of 128x64 (23,330,816 bytes) fits. */
+#define SDFR_NOALLOC_SCRATCH_BYTES (24ll << 20)
+
+/* sdfr_render without a workspace argument and without any allocation: no
+ * counterpart in the reference. For callers that cannot allocate device
+ * memory — code under hipGraph capture, tight serving loops, harnesses that
+ * forbid hipMalloc. The workspace is a static device array of
+ * SDFR_NOALLOC_SCRATCH_BYTES that each GPU holds until the process ends;
+ * renders whose sdfr_workspace_bytes() exceed it are refused (-2) before any
+ * launch. Every call on one GPU shares that GPU's array: calls that overlap
+ * on one GPU (other streams, other threads, other handles) race and must be
+ * serialised by the caller. The grid's device must be current. Otherwise as
+ * sdfr_render: asynchronous on `stream`, 0 or < 0 with sdfr_last_error(). */
+SDFR_API int32_t sdfr_render_noalloc(const SdfrGrid* grid, const SdfrCam* cam,
+                                     const SdfrPoses* poses, const SdfrImage* image,
+                                     void* stream);
+
 /* Reads the handle's grid copy back as nz*ny*nx fp32 values in [nz][ny][nx]
  * order: exactly the values the march samples (fp16 widened, r16 decoded).
  * The reference's kernel samples its device tensor GpuLidar.sdf_flat

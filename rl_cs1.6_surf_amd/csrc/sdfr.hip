@@ -62,6 +62,7 @@
 #include <stdio.h>
 #include <string.h>
 
+#include <mutex>
 #include <type_traits>
 
 #include "../../include/sdfr.h"
@@ -1452,6 +1453,42 @@ int32_t render_impl(const char* fn, const SdfrGrid* grid, const SdfrCam* cam, co
     return 0;
 }
 
+// ---------------------------------------------------- allocation-free render --
+// sdfr_render_noalloc takes its workspace (ray tables and tile order) from
+// this file-scope device array instead of the caller. Each GPU the library
+// runs on holds its own copy until the process ends; the host reaches it only
+// through the per-device address hipGetSymbolAddress reports (the array's
+// name is a host-side stand-in, not a device address). Every call on one GPU
+// shares that GPU's copy. Nothing in it needs clearing between calls: the
+// ray-setup launch writes every entry a render reads.
+constexpr int64_t kScratchBytes = SDFR_NOALLOC_SCRATCH_BYTES;
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices];
+
+// The current device's copy of `scratch`, looked up once per device.
+int32_t scratch_for_current_device(const char* fn, const SdfrGrid* grid, void** out) {
+    int dev = -1;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return fail(-4, "%s: hipGetDevice failed: %s", fn, hipGetErrorString(e));
+    if (dev != grid->device)
+        return fail(-2, "%s: the grid lives on device %d but device %d is current", fn,
+                    grid->device, dev);
+    if (dev < 0 || dev >= kMaxDevices) return fail(-2, "%s: device %d out of range", fn, dev);
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_ptr[dev]) {
+        void* p = nullptr;
+        e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !p)
+            return fail(-4, "%s: hipGetSymbolAddress(scratch) failed: %s", fn, hipGetErrorString(e));
+        g_scratch_ptr[dev] = p;
+    }
+    *out = g_scratch_ptr[dev];
+    return 0;
+}
+
 }  // namespace
 
 // ================================================================ C ABI ==
@@ -1716,6 +1753,25 @@ SDFR_API int32_t sdfr_render(const SdfrGrid* grid, const SdfrCam* cam, const Sdf
                              void* stream) {
     g_err[0] = '\0';
     return render_impl("sdfr_render", grid, cam, poses, image, workspace, workspace_size, stream);
+}
+
+SDFR_API int32_t sdfr_render_noalloc(const SdfrGrid* grid, const SdfrCam* cam,
+                                     const SdfrPoses* poses, const SdfrImage* image,
+                                     void* stream) {
+    g_err[0] = '\0';
+    const char* fn = "sdfr_render_noalloc";
+    if (!grid || !grid->data) return fail(-1, "%s: null grid handle", fn);
+    int32_t rc = check_cam_poses(fn, cam, poses);
+    if (rc) return rc;
+    const int64_t need = workspace_bytes(cam->width, cam->height, poses->n_envs);
+    if (need > kScratchBytes)
+        return fail(-2, "%s: %d envs of %dx%d need %lld bytes of workspace; the static scratch "
+                    "holds %lld (use sdfr_render with a workspace)", fn, poses->n_envs,
+                    cam->width, cam->height, (long long)need, (long long)kScratchBytes);
+    void* ws = nullptr;
+    rc = scratch_for_current_device(fn, grid, &ws);
+    if (rc) return rc;
+    return render_impl(fn, grid, cam, poses, image, ws, kScratchBytes, stream);
 }
 
 SDFR_API int32_t sdfr_grid_read(const SdfrGrid* grid, float* out, void* stream) {

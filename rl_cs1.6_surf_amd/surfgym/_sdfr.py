@@ -19,6 +19,7 @@ PKG_ROOT = Path(__file__).resolve().parents[1]
 LIB_PATH = PKG_ROOT / "lib" / "libsdfr.so"
 
 ABI_VERSION = 12
+NOALLOC_SCRATCH_BYTES = 24 << 20   # SDFR_NOALLOC_SCRATCH_BYTES
 
 # element types (SDFR_* in sdfr.h)
 F32, F16, BF16, I32, I64, U8, F64, U16, R16 = 0, 1, 2, 3, 4, 5, 6, 7, 8
@@ -30,7 +31,8 @@ ORDER_LAUNCH, ORDER_LOOKAHEAD = 0, 1
 EXPORTS = ("sdfr_abi_version", "sdfr_last_error", "sdfr_grid_create", "sdfr_grid_destroy",
            "sdfr_grid_bytes", "sdfr_grid_attach_surfnz", "sdfr_grid_set_schedule",
            "sdfr_grid_set_tile_order", "sdfr_grid_set_march_events", "sdfr_render_rays_per_lane",
-           "sdfr_workspace_bytes", "sdfr_render", "sdfr_ray_dirs", "sdfr_grid_read",
+           "sdfr_workspace_bytes", "sdfr_render", "sdfr_render_noalloc", "sdfr_ray_dirs",
+           "sdfr_grid_read",
            "sdfr_edt_workspace_bytes",
            "sdfr_edt", "sdfr_edt_last_error", "sdfr_goal_workspace_bytes", "sdfr_goal_bake",
            "sdfr_goal_sample", "sdfr_goal_last_error")
@@ -114,6 +116,9 @@ def load(path: Path | str | None = None):
     lib.sdfr_render.restype = i32
     lib.sdfr_render.argtypes = [vp, ctypes.POINTER(Cam), ctypes.POINTER(Poses),
                                 ctypes.POINTER(Image), vp, i64, vp]
+    lib.sdfr_render_noalloc.restype = i32
+    lib.sdfr_render_noalloc.argtypes = [vp, ctypes.POINTER(Cam), ctypes.POINTER(Poses),
+                                        ctypes.POINTER(Image), vp]
     lib.sdfr_grid_read.restype = i32
     lib.sdfr_grid_read.argtypes = [vp, vp, vp]
     lib.sdfr_ray_dirs.restype = i32

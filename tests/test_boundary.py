@@ -33,6 +33,8 @@ def test_abi_version_matches_the_binding():
     text = (ROOT / "include" / "sdfr.h").read_text()
     assert int(re.search(r"#define SDFR_ABI_VERSION (\d+)", text).group(1)) == _sdfr.ABI_VERSION
     assert lib.sdfr_abi_version() == _sdfr.ABI_VERSION
+    m = re.search(r"#define SDFR_NOALLOC_SCRATCH_BYTES \((\d+)ll << (\d+)\)", text)
+    assert int(m.group(1)) << int(m.group(2)) == _sdfr.NOALLOC_SCRATCH_BYTES
 
 
 def test_binding_structs_match_the_header_layout(tmp_path):
@@ -104,6 +106,8 @@ def test_schedule_and_tile_order_reject_a_null_handle_without_a_device():
     from surfgym import _sdfr
     lib = _sdfr.load()
     assert lib.sdfr_grid_read(None, None, None) == -1
+    assert "null grid" in _sdfr.last_error()
+    assert lib.sdfr_render_noalloc(None, None, None, None, None) == -1
     assert "null grid" in _sdfr.last_error()
     assert lib.sdfr_grid_set_schedule(None, 2, 16, 0) == -1      # no slot schedule any more
     assert lib.sdfr_grid_set_tile_order(None, _sdfr.ORDER_LOOKAHEAD, -1) == -1
