@@ -36,6 +36,22 @@ def test_empty_and_full_grids(dev):
         assert np.array_equal(got, ref.astype(np.float32)), occ.shape
 
 
+@pytest.mark.parametrize("shape", [(64, 512, 512), (256, 32, 512)])
+def test_both_pass_algorithms_match_scipy(dev, shape):
+    """Each of the y and z passes walks the parabola envelope when it has
+    many lines and searches a window per output when it has few (the switch
+    is at 512 lines per CU: 131,072 on 256 CUs). (64, 512, 512): y by window
+    (32,768 lines), z by envelope (262,144); (256, 32, 512): y by envelope
+    (131,072), z by window (16,384). Both equal scipy bit for bit."""
+    rng = np.random.default_rng(sum(shape))
+    occ = (rng.random(shape) < 0.002).astype(np.uint8)
+    occ[:, :, : shape[2] // 8] |= (rng.random((shape[0], shape[1], 1)) < 0.3).astype(np.uint8)
+    print(f"case edt both algorithms {shape}", flush=True)
+    ref = edt.bake(occ, 16.0).astype(np.float32)
+    got = vision.sdf_from_occupancy(occ, 16.0, device=dev, dtype=torch.float32).cpu().numpy()
+    assert np.array_equal(got, ref)
+
+
 def test_scene_occupancy_matches_scipy_and_renders(dev):
     """The ramp_field scene's solids (256x256x128, 8.4 M voxels): baked on the
     GPU, equal to scipy's bake, and renderable as is."""
