@@ -348,9 +348,10 @@ def bench_goal(args, dev):
 
 
 def alg_bytes_per_load(store):
-    """Grid bytes one sample reads: the voxel (4 B fp32, 2 B fp16), or for
-    r16 bricks the 2 B code and its brick's 8 B header (base, scale)."""
-    return {"f32": 4, "f16": 2, "r16": 10}[store]
+    """Grid bytes per sample: the stored size of a voxel, 4 B fp32, 2 B fp16,
+    and for r16 bricks the 2 B code plus its share of the brick's 8 B header
+    (base, scale) over 64 voxels."""
+    return {"f32": 4.0, "f16": 2.0, "r16": 2.0 + 8.0 / 64.0}[store]
 
 
 def measure_render(w, args, dev, *, graph, steps, warmup, out_shape=None, sc=None):
@@ -393,7 +394,7 @@ def measure_render(w, args, dev, *, graph, steps, warmup, out_shape=None, sc=Non
     del taps
     rays = n * w.width * w.height
     out_b = 2 if w.out_dtype == "bf16" else 4
-    alg_bytes = loads * alg_bytes_per_load(w.store) + rays * out_b + n * 24
+    alg_bytes = int(loads * alg_bytes_per_load(w.store)) + rays * out_b + n * 24
     _log(f"[bench] census: {loads} loads, mean {loads / rays:.2f}/ray, max {max_taps}")
 
     step = lambda: lid.render(origin, yaw, pitch, duck, out=out)   # noqa: E731
@@ -527,7 +528,9 @@ def main(argv=None):
     w = synth.WORKLOADS[args.workload]
     if args.bake:
         return bench_bake(args, w, dev)
-    r = measure_render(w, args, dev, graph=args.graph, steps=args.steps, warmup=args.warmup)
+    shape = {n: s for n, _, s in OTHER_CONFIGS}.get(w.name)
+    r = measure_render(w, args, dev, graph=args.graph, steps=args.steps, warmup=args.warmup,
+                       out_shape=shape)
     sc, lid = r.pop("sc"), r.pop("lid")
     n, rays = r["envs"], r["rays"]
     ms_per_step, kernel_ms = r["ms_per_step"], r["march_kernel_ms_avg"]
