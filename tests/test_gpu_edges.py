@@ -1,0 +1,79 @@
+"""GPU edge cases of the render against the oracle: degenerate grid shapes
+(one voxel thick along any axis, a single voxel, partial bricks) in every
+store and layout, and eyes outside the grid on every side (every sample then
+reads the clamped border voxel first, vision.py:644-646)."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from surfgym import vision
+
+pytestmark = pytest.mark.gpu
+
+_STORES = [(torch.float32, "f32", "brick4"), (torch.float32, "f32", "linear"),
+           (torch.float16, "f16", "brick4"), ("r16", "r16", "brick4")]
+
+
+def _field(shape, seed):
+    """A distance-like field: distance (16 u cells) to a few random solid
+    voxels, 0 on them."""
+    rng = np.random.default_rng(seed)
+    nz, ny, nx = shape
+    zz, yy, xx = np.meshgrid(np.arange(nz), np.arange(ny), np.arange(nx), indexing="ij")
+    pts = rng.integers(0, [nz, ny, nx], (max(1, int(np.prod(shape)) // 40), 3))
+    d = np.full(shape, np.inf)
+    for z, y, x in pts:
+        d = np.minimum(d, np.sqrt((zz - z) ** 2 + (yy - y) ** 2 + (xx - x) ** 2))
+    return (d * 16.0).astype(np.float32)
+
+
+def _poses(shape, n, seed, outside=False):
+    rng = np.random.default_rng(seed)
+    ext = np.array(shape[::-1], np.float64) * 16.0
+    if outside:
+        # eyes beyond each face of the grid (and beyond corners)
+        o = rng.uniform(-0.5, 1.5, (n, 3)) * ext
+        o[:, rng.integers(0, 3)] = np.where(rng.random(n) < 0.5, -200.0, ext.max() + 200.0)
+    else:
+        o = rng.uniform(0.0, 1.0, (n, 3)) * ext
+    o[:, 2] -= 17.0
+    yaw = rng.uniform(-180, 180, n).astype(np.float32)
+    pitch = rng.uniform(-70, 30, n).astype(np.float32)
+    duck = (rng.random(n) < 0.5).astype(np.float32)
+    return o.astype(np.float32), yaw, pitch, duck
+
+
+@pytest.mark.parametrize("shape", [(1, 1, 1), (1, 5, 3), (4, 1, 9), (7, 6, 1), (5, 9, 13),
+                                   (2, 33, 2)])
+@pytest.mark.parametrize("gdt,store,layout", _STORES)
+def test_degenerate_grid_shapes(dev, shape, gdt, store, layout):
+    g = _field(shape, sum(shape))
+    n = 5
+    o, yaw, pitch, duck = _poses(shape, n, 7)
+    print(f"case edges shape={shape} store={store} layout={layout}", flush=True)
+    kw = dict(width=24, height=10, range_units=900.0, near_range=400.0, max_steps=48)
+    lid = vision.GpuLidar.from_grid(g, np.zeros(3), 16.0, grid_dtype=gdt, layout=layout,
+                                    device=dev, **kw)
+    for order in ("lookahead", "launch"):
+        lid.set_tile_order(order, min_tiles=0)
+        got = lid.render(*[torch.as_tensor(a, device=dev) for a in (o, yaw, pitch, duck)])
+        want, _ = oracle.render(g, np.zeros(3), 16.0, o, yaw, pitch, duck, store=store, **kw)
+        assert np.array_equal(got.cpu().numpy(), want), order
+
+
+@pytest.mark.parametrize("gdt,store,layout", _STORES)
+def test_eyes_outside_the_grid(dev, gdt, store, layout):
+    shape = (20, 24, 28)
+    g = _field(shape, 3)
+    n = 64
+    o, yaw, pitch, duck = _poses(shape, n, 11, outside=True)
+    print(f"case edges eyes outside store={store} layout={layout}", flush=True)
+    kw = dict(width=32, height=16, range_units=1500.0, near_range=600.0, max_steps=64)
+    lid = vision.GpuLidar.from_grid(g, np.full(3, -8.0), 16.0, grid_dtype=gdt, layout=layout,
+                                    device=dev, **kw)
+    got = lid.render(*[torch.as_tensor(a, device=dev) for a in (o, yaw, pitch, duck)])
+    want, _ = oracle.render(g, np.full(3, -8.0), 16.0, o, yaw, pitch, duck, store=store, **kw)
+    assert np.array_equal(got.cpu().numpy(), want)
