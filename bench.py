@@ -38,7 +38,7 @@ def _log(msg):
     print(msg, file=sys.stderr, flush=True)
 
 
-def cpu_baseline(w, sc, envs, repeats=3):
+def cpu_baseline(w, sc, envs, repeats=5):
     """Lockstep torch render (the reference's CPU path shape) on host cores."""
     import torch
     from oracle import lockstep

@@ -16,10 +16,20 @@ its goal field:
   (``_render_torch``, vision.py:626-666): torch tensors over all rays in
   lockstep, with a host ``any()`` check every 8 steps. It is the CPU
   baseline that bench.py times.
+* :func:`as_stored` / :func:`r16_encode` / :func:`r16_decode` — the values
+  the renderer reads from each grid store (fp32; fp16 as torch rounds it,
+  vision.py:476; the r16 bricks, a storage format of this renderer).
+* :mod:`oracle.edt` — the reference's scipy bake call (vision.py:428-438).
 
-Every function here is pinned by tests/test_oracle.py (closed forms,
-invariants, brute force on tiny inputs) and by the committed fixtures in
-tests/golden/.
+Where each is pinned (closed forms, invariants, brute force on tiny inputs,
+an independent second implementation, planted mistakes):
+
+* render, ray_dirs, offsets, encode — tests/test_oracle.py and the committed
+  fixtures in tests/golden/ (tests/test_golden.py);
+* lockstep — tests/test_oracle_lockstep.py, against render;
+* r16_encode / r16_decode — tests/test_oracle_store.py;
+* edt — tests/test_oracle.py (exhaustive nearest-solid search);
+* goal — tests/test_oracle_goal.py.
 """
 from __future__ import annotations
 
