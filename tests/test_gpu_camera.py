@@ -130,3 +130,52 @@ def test_the_bench_poses_exercise_the_march(dev):
     assert d.min().item() < 0.05, "no near hits"
     assert d.max().item() > 1.0, "nothing beyond the near range"
     assert 0.02 < far < 0.98, far
+
+
+def test_the_pinhole_flag_allocates_only_its_tables(dev, shelf):
+    """Equiangular lidars hold the grid, mins and the two angle tables as
+    tensors; the pinhole flag adds exactly the tangent-plane tables
+    (u = tan(hfov/2) * (2c/(W-1) - 1), v = tan(vfov/2) * (1 - 2r/(H-1)),
+    vision.py:510-529), and an equiangular render is unchanged by the
+    feature existing (tests/python/test_pinhole.py:251-263)."""
+    off = vision.GpuLidar.from_grid(shelf, np.zeros(3), CELL, width=8, height=4, device=dev)
+    on = vision.GpuLidar.from_grid(shelf, np.zeros(3), CELL, width=8, height=4, pinhole=True,
+                                   device=dev)
+    base = {k for k, v in vars(off).items() if torch.is_tensor(v)}
+    assert base == {"sdf_flat", "mins", "yoff", "poff"}
+    assert {k for k, v in vars(on).items() if torch.is_tensor(v)} - base == {"uoff", "voff"}
+    assert off.pinhole is False and on.pinhole is True
+    th, tv = np.tan(np.radians(60.0)), np.tan(np.radians(45.0))
+    assert np.allclose(on.uoff.cpu().numpy(), th * (2 * np.arange(8) / 7 - 1), atol=1e-6)
+    assert np.allclose(on.voff.cpu().numpy(), tv * (1 - 2 * np.arange(4) / 3), atol=1e-6)
+    args = [torch.as_tensor(a, device=dev) for a in
+            (np.array([[300.0, 600.0, 300.0]], np.float32), np.zeros(1, np.float32),
+             np.array([-20.0], np.float32), np.zeros(1, np.float32))]
+    assert off.render(*args).shape == (1, 4, 8) and on.render(*args).shape == (1, 4, 8)
+
+
+@pytest.mark.parametrize("W,H", [(1, 9), (9, 1), (1, 1)])
+def test_a_one_pixel_axis_looks_along_the_view(dev, shelf, W, H):
+    """A one-pixel axis has its single ray on the view's centre line in both
+    cameras (pinhole u = 0 / v = 0, equiangular offset 0;
+    tests/python/test_pinhole.py:266-273)."""
+    for pin in (False, True):
+        lid = vision.GpuLidar.from_grid(shelf, np.zeros(3), CELL, width=W, height=H,
+                                        pinhole=pin, device=dev)
+        d = lid.ray_dirs(torch.tensor([30.0]), torch.tensor([-12.0]))[0].cpu().numpy()
+        y, p = np.radians(30.0), np.radians(-12.0)
+        view = np.array([np.cos(p) * np.cos(y), np.cos(p) * np.sin(y), np.sin(p)])
+        if W == 1:
+            col = d[:, 0, :]
+            # every ray of the single column lies in the vertical plane of the view
+            assert np.abs(col[:, 0] * np.sin(y) - col[:, 1] * np.cos(y)).max() < 1e-6
+        if H == 1:
+            row = d[0, :, :]
+            if pin:
+                # the single row of the pinhole camera lies in the view's
+                # horizontal-tilted plane through the centre ray
+                assert np.abs(row @ np.cross(view, [-np.sin(y), np.cos(y), 0.0])).max() < 1e-6
+            else:
+                assert np.allclose(row[:, 2], np.sin(p), atol=1e-7)
+        if W % 2 == 1 and H % 2 == 1:
+            assert np.abs(d[H // 2, W // 2] - view).max() < 1e-6
