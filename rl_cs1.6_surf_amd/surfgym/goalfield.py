@@ -310,7 +310,8 @@ def _mask_kill_volumes(occ, mins, cell: float, bsp: Path):
             m = np.asarray(hit).reshape(box.shape)
             walled += int((m & (box == 0)).sum())
             box[m] = 1
-    print(f"goal graph: {len(kills)} kill volumes hull-masked ({walled} free voxels -> wall)")
+    print(f"[goalfield] {walled} free voxels inside {len(kills)} kill triggers made solid "
+          "for the geodesic")
     return occ
 
 
@@ -337,8 +338,8 @@ def build_goal_field(core, zone, cell: float, cache_dir=None, device="cuda",
         occ = _mask_kill_volumes(occ, np.asarray(mins, np.float64), cell, bsp)
     field = goal_field_from_occupancy(occ, mins, zone, cell, device=device)
     info = field.bake_info
-    print(f"goal field: {info['sweeps']} sweeps, {info['n_seed']} seed voxels, "
-          f"max geodesic {field.reach_max:.0f}u")
+    print(f"[goalfield] GPU bake: {info['n_seed']} seed voxels, {info['sweeps']} wavefront "
+          f"sweeps, farthest reachable voxel {field.reach_max:.0f} u")
     q = field.grid_q.cpu().numpy().view(np.uint16)
     np.savez_compressed(cache_file, grid=q, quant=np.float32(info["quant"]),
                         mins=mins, cell=np.float32(cell),

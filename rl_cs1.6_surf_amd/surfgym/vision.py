@@ -178,7 +178,7 @@ def slab_occupancy(core, cell: float = 16.0, cache_dir=None):
         occ[lo[2]:hi[2], lo[1]:hi[1], lo[0]:hi[0]] = 1
         n_thin += 1
     if n_thin:
-        print(f"slab occupancy: rasterized {n_thin} thin solid entities")
+        print(f"[vision] {n_thin} thin solid brushes filled into the slab occupancy")
     np.savez_compressed(path, occ=occ, mins=mins, sig=np.str_(sig))
     return occ, mins
 
