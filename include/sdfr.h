@@ -67,10 +67,10 @@ enum {
 /* Work schedules of sdfr_render (both give identical results). */
 enum {
     SDFR_SCHED_PERSISTENT = 0, /* persistent waves refilling ended rays' lanes */
-    SDFR_SCHED_TILES = 1       /* default: launch-scheduled waves of 8x8 pixel tiles */
+    SDFR_SCHED_TILES = 1       /* default: launch-scheduled waves of 16x4 pixel tiles */
 };
 
-/* The order in which the tiles schedule takes 8x8 pixel tiles. */
+/* The order in which the tiles schedule takes 16x4 pixel tiles. */
 enum {
     SDFR_ORDER_LAUNCH = 0,    /* env by env, as the batch is laid out */
     SDFR_ORDER_LOOKAHEAD = 1  /* default: sorted by where each tile's centre ray is 1.2 x near
@@ -183,7 +183,7 @@ SDFR_API int32_t sdfr_render_rays_per_lane(const SdfrGrid* grid, const SdfrCam* 
 /* Chooses the tile order of later renders on this handle (SDFR_ORDER_*,
  * default SDFR_ORDER_LOOKAHEAD). The lookahead order costs two small sort
  * launches per render, so it applies only to renders of at least
- * `min_tiles` 8x8 tiles (< 0: the library default, 65536 = 512 envs of
+ * `min_tiles` tiles of 16x4 pixels (< 0: the library default, 65536 = 512 envs of
  * 128x64; 0: always); smaller renders take the launch order. Applies to the
  * tiles schedule and the surf-mask variant; results do not depend on it.
  * Synchronous; 0 or < 0. No reference counterpart. */
@@ -203,7 +203,8 @@ SDFR_API int64_t sdfr_grid_bytes(const SdfrGrid* grid);
 
 /* Device bytes of the workspace sdfr_render needs for n_envs envs of this
  * camera: per env (W + H + 4) float2 of ray tables, then for the tile order
- * one int32, one uint16 and one uint32 per 8x8 tile (each part 256-byte
+ * one int32, one uint16 and one uint32 per tile (16x4 pixels; tiles come in
+ * 2x2 quads, ceil(W/32) * ceil(H/8) * 4 per env; each part 256-byte
  * aligned). < 0 on bad arguments. The tile order's bucket counts live in
  * the grid handle. */
 SDFR_API int64_t sdfr_workspace_bytes(const SdfrCam* cam, int32_t n_envs);

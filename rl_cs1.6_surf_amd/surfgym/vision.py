@@ -285,7 +285,7 @@ class GpuLidar:
     * ``hit_eps`` / ``min_step`` — the step rule's constants, 0.6*cell and
       0.3*cell by default (vision.py:87-88);
     * ``schedule`` / ``refill_lanes`` / ``rays_per_lane`` — how the kernel
-      schedules rays: launch-scheduled waves of 8x8 pixel "tiles", each lane
+      schedules rays: launch-scheduled waves of 16x4 pixel "tiles", each lane
       marching ``rays_per_lane`` rays at once (default None: each render
       picks 1 for grids above 192 MiB and for renders under 512 envs of
       128x64, else 2; see :meth:`effective_rays_per_lane`); or "persistent"
@@ -413,7 +413,7 @@ class GpuLidar:
         """Switch the ray schedule of later renders (results are unchanged).
         ``rays_per_lane=None`` lets each render choose (the library's
         default: 1 for grids above 192 MiB and for renders of fewer than
-        65536 8x8 tiles, else 2); ``rays_per_lane`` then reads None."""
+        65536 16x4 tiles, else 2); ``rays_per_lane`` then reads None."""
         if schedule not in _SCHEDULES:
             raise ValueError(f"schedule must be one of {sorted(_SCHEDULES)}, got {schedule!r}")
         rpl = 0 if rays_per_lane is None else int(rays_per_lane)
@@ -433,7 +433,7 @@ class GpuLidar:
         return r
 
     def set_tile_order(self, order: str = "lookahead", min_tiles: int | None = None) -> None:
-        """The order the tiles schedule takes 8x8 pixel tiles in: "launch"
+        """The order the tiles schedule takes 16x4 pixel tiles in: "launch"
         (env by env) or "lookahead" (sorted by where each tile's centre ray
         is 1.2 x near units out, so each XCD's cache serves one part of the
         map). The sort costs two small launches, so "lookahead" applies to

@@ -125,7 +125,7 @@ def test_render_rejects_bad_arguments_without_a_device():
     rc = lib.sdfr_render(None, ctypes.byref(_cam()), ctypes.byref(_poses()), ctypes.byref(img),
                          None, 0, None)
     assert rc == -1 and "grid" in _sdfr.last_error()
-    # ray tables, then an int32, a uint16 and a uint32 per 8x8 tile (parts 256-byte aligned)
+    # ray tables, then an int32, a uint16 and a uint32 per 16x4 tile (parts 256-byte aligned)
     assert lib.sdfr_workspace_bytes(ctypes.byref(_cam()), 2048) == (
         2048 * (128 + 64 + 4) * 8 + 2048 * 128 * 4 + 2048 * 128 * 2 + 2048 * 128 * 4)
     c = _cam(width=9, height=5)

@@ -126,9 +126,9 @@ def test_f16_slot_packing_is_exact(dev, name, n, size):
     """fp16 grids march with slot packing (a wave's two tiles merged into one
     slot once their live rays fit 64 lanes): images and per-ray load counts
     equal the oracle's on the f16-rounded grid bit for bit, in both tile
-    orders. 37x19 images give waves whose two tiles lie in different envs
-    (no packing there) and lanes without a pixel; 8x8 images give one tile
-    per env."""
+    orders. 37x19 images give quads of tiles partly outside the image
+    (lanes and whole tiles without a pixel); 8x8 images give one quad per
+    env, half of it outside."""
     w, sc = _scene(name)
     ps = w.poses(sc, n)
     W, H = size if size else (w.width, w.height)
@@ -328,7 +328,7 @@ def test_step_rule_corners_are_exact_in_every_schedule(dev, max_steps, hit_eps, 
 
 @pytest.mark.parametrize("W,H,n", [(9, 5, 3), (33, 33, 2), (1, 1, 5), (20, 12, 7)])
 def test_ragged_images_match_the_oracle(dev, W, H, n):
-    """Image sizes that do not fill whole 8x8 tiles, and tiny N."""
+    """Image sizes that do not fill whole 16x4 tiles, and tiny N."""
     w, sc = _scene("small_ramps")
     ps = w.poses(sc, n)
     _say(f"case ragged {W}x{H} n={n}")
@@ -449,8 +449,9 @@ def test_tile_order_with_pinhole_ragged_and_surf_mask(dev):
     o, y = torch.as_tensor(ps.origin, device=dev), torch.as_tensor(ps.yaw, device=dev)
     p, d = torch.as_tensor(ps.pitch, device=dev), torch.as_tensor(ps.ducked, device=dev)
     snz = np.random.default_rng(3).integers(0, 128, sc.sdf.shape).astype(np.int8)
-    # 37x19 and 8x8 over 5 envs give odd tile counts (75 and 5): the last run
-    # of the order holds one tile, and every tile must still be marched once
+    # 37x19 and 8x8 over 5 envs leave quads of tiles partly (8x8: half)
+    # outside the image: tiles without a pixel are ordered and marched as
+    # empty, and every pixel must still be marched once
     for kw in (dict(pinhole=True, rays_per_lane=2), dict(width=37, height=19, rays_per_lane=2),
                dict(width=8, height=8, rays_per_lane=2),
                dict(width=37, height=19, rays_per_lane=1), dict(width=8, height=8, rays_per_lane=1),
