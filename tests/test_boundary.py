@@ -130,6 +130,11 @@ def test_render_rejects_bad_arguments_without_a_device():
         2048 * (128 + 64 + 4) * 8 + 2048 * 128 * 4 + 2048 * 128 * 2 + 2048 * 128 * 4)
     c = _cam(width=9, height=5)
     assert lib.sdfr_workspace_bytes(ctypes.byref(c), 3) == 512 + 256 + 256 + 256
+    # tiles come in 2x2 quads of 32x8 pixels: 40x9 is 2 x 2 quads, 16 tiles per env
+    c = _cam(width=40, height=9)
+    a256 = lambda v: (v + 255) // 256 * 256   # noqa: E731
+    assert lib.sdfr_workspace_bytes(ctypes.byref(c), 100) == (
+        a256(100 * (40 + 9 + 4) * 8) + a256(1600 * 4) + a256(1600 * 2) + a256(1600 * 4))
     assert lib.sdfr_workspace_bytes(ctypes.byref(_cam()), 0) < 0
     # the grid check comes first; the argument checks are shared with sdfr_ray_dirs
     cases = [
