@@ -459,9 +459,13 @@ def measure_render(w, args, dev, *, graph, steps, warmup, out_shape=None, sc=Non
     return res
 
 
-def config_summary(r):
-    """A workload's figures for the `configs` object of the JSON line."""
+def config_summary(r, traffic=None, traffic_src=None, limiter=None):
+    """A workload's figures for the `configs` object of the JSON line; with
+    its profile's L2-miss traffic per launch (None when the profile is
+    stale), the rate that traffic streams at over the march kernel's
+    average duration, and the unit the profile names as the limit."""
     achieved = r["alg_bytes"] / (r["march_kernel_ms_avg"] * 1e-3) / 1e9
+    rate = traffic / (r["march_kernel_ms_avg"] * 1e-3) / 1e9 if traffic else None
     return {"envs": r["envs"], "rays": r["rays"], "grid": r["grid"], "out": r["out"],
             "out_shape": r["out_shape"], "graph": r["graph"],
             "ms_per_batch": round(r["ms_per_step"], 5),
@@ -470,6 +474,10 @@ def config_summary(r):
             "grid_loads_per_ray": round(r["loads"] / r["rays"], 4),
             "alg_bytes_per_launch": r["alg_bytes"],
             "alg_frac_of_hbm_peak": round(achieved / HBM_PEAK_GBS, 5),
+            "traffic_bytes_per_launch": traffic,
+            "traffic_gbs": round(rate, 1) if rate else None,
+            "traffic_source": traffic_src,
+            "limiter": limiter.get("unit") if limiter else None,
             "rays_per_lane": r["rpl"]}
 
 
@@ -572,6 +580,8 @@ def main(argv=None):
                    "march_kernel_ms_avg": round(kernel_ms, 5)},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 5), "traffic": traffic,
+                     "traffic_gbs": (round(traffic / (kernel_ms * 1e-3) / 1e9, 1)
+                                     if traffic else None),
                      "traffic_source": traffic_src,
                      "alg_bytes_per_launch": r["alg_bytes"],
                      "copy_gbs": round(copy_gbs, 1) if copy_gbs else None,
@@ -588,9 +598,12 @@ def main(argv=None):
             cw = synth.WORKLOADS[name]
             cr = measure_render(cw, args, dev, graph=graph, steps=args.config_steps,
                                 warmup=min(args.warmup, 5), out_shape=shape)
-            cr.pop("lid")
+            order = cr.pop("lid").tile_order
             cr.pop("sc")
-            configs[name] = config_summary(cr)
+            ct, ct_src = profiled(f"{name} {args.schedule} rpl={cr['rpl']} {args.layout} {cw.store}"
+                                  f" order={order}", traffic_tab, "bytes")
+            cl, _ = profiled(name, limiter_tab)
+            configs[name] = config_summary(cr, ct, ct_src, cl)
             torch.cuda.empty_cache()
         res["configs"] = configs
     if not args.no_cpu:

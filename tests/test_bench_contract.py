@@ -80,3 +80,18 @@ def test_other_configurations_cover_the_metric_workloads():
     assert graph["ramp_field_r16_bf16"] is True
     shape = {n: s for n, _, s in bench.OTHER_CONFIGS}["ramp_field_r16_bf16"]
     assert shape(8192) == (8192, 1, 64, 128)
+
+
+def test_config_summary_carries_the_profiled_traffic_rate():
+    r = {"envs": 2048, "rays": 16777216, "grid": "g", "out": "f32", "out_shape": [2048, 64, 128],
+         "graph": False, "ms_per_step": 2.0, "march_kernel_ms_avg": 1.5, "loads": 335544320,
+         "alg_bytes": 1_500_000_000, "rpl": 1}
+    s = bench.config_summary(r, 15_000_000_000, {"profile": "p", "current": True},
+                             {"unit": "L2-miss traffic", "busy": 0.9})
+    assert s["traffic_bytes_per_launch"] == 15_000_000_000
+    assert s["traffic_gbs"] == 10000.0          # 15 GB over 1.5 ms
+    assert s["alg_frac_of_hbm_peak"] == 0.125   # 1 TB/s of 8
+    assert s["limiter"] == "L2-miss traffic" and s["g_rays_per_s"] == round(16777216 / 2e-3 / 1e9, 4)
+    stale = bench.config_summary(r)
+    assert stale["traffic_bytes_per_launch"] is None and stale["traffic_gbs"] is None
+    assert stale["limiter"] is None
