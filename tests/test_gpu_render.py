@@ -8,7 +8,6 @@ operation sequence. Reference semantics: python/surfgym/vision.py:59-116,
 """
 from __future__ import annotations
 
-
 import numpy as np
 import pytest
 import torch
