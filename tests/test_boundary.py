@@ -143,6 +143,8 @@ def test_render_rejects_bad_arguments_without_a_device():
         (dict(near=0.0), {}, "near"),
         (dict(camera=5), {}, "camera"),
         ({}, dict(n_envs=0), "n_envs"),
+        (dict(width=8192, height=4096), {}, "image too large"),
+        ({}, dict(n_envs=262144), "too many rays"),   # 2^31 rays of 128x64
         ({}, dict(origin=None), "null pose"),
         ({}, dict(ducked_dtype=42), "ducked dtype"),
     ]

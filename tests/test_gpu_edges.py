@@ -77,3 +77,31 @@ def test_eyes_outside_the_grid(dev, gdt, store, layout):
     got = lid.render(*[torch.as_tensor(a, device=dev) for a in (o, yaw, pitch, duck)])
     want, _ = oracle.render(g, np.full(3, -8.0), 16.0, o, yaw, pitch, duck, store=store, **kw)
     assert np.array_equal(got.cpu().numpy(), want)
+
+
+def test_the_largest_batch_renders_every_env(dev):
+    """The largest batch the library accepts at 128x64 (2^31 - 1 rays):
+    262,140 envs, four distinct poses repeated, so the image offsets reach
+    the top of the int32 range. Every env must equal the oracle's image of
+    its pose (batch independence, tests/python/test_lidar_march.py:161-169,
+    at the size limit)."""
+    from surfgym import synth
+    w = synth.WORKLOADS["small_ramps"]
+    sc = w.scene()
+    ps = w.poses(sc, 4)
+    n = 262_140
+    assert n * w.width * w.height <= 2 ** 31 - 1 < (n + 4) * w.width * w.height
+    print(f"case edges largest batch n={n}", flush=True)
+    kw = dict(width=w.width, height=w.height, range_units=w.range_units, near_range=w.near_range,
+              max_steps=w.max_steps, hit_eps=w.hit_eps)
+    want, _ = oracle.render(sc.sdf, sc.mins, sc.cell, ps.origin, ps.yaw, ps.pitch, ps.ducked, **kw)
+    lid = vision.GpuLidar.from_grid(sc.sdf, sc.mins, sc.cell, grid_dtype=torch.float32, device=dev,
+                                    **kw)
+    rep = lambda a: torch.as_tensor(a, device=dev).repeat((n // 4,) + (1,) * (a.ndim - 1))  # noqa: E731
+    got = lid.render(rep(ps.origin), rep(ps.yaw), rep(ps.pitch), rep(ps.ducked))
+    assert got.shape == (n, w.height, w.width)
+    ref = torch.as_tensor(want, device=dev)
+    assert torch.equal(got.view(n // 4, 4, w.height, w.width)[-1], ref)
+    assert bool((got.view(n // 4, 4, w.height, w.width) == ref).all())
+    del got
+    torch.cuda.empty_cache()
