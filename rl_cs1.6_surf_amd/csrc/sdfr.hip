@@ -93,6 +93,7 @@ constexpr int kSpillBlocksPerCU = 12;
 // Tile order: 16 cells per axis at most, Morton-numbered buckets.
 constexpr int kOrderCellsLog = 4;
 constexpr int kOrderBuckets = 1 << (3 * kOrderCellsLog);
+static_assert(kOrderBuckets % 256 == 0, "the sort blocks' 256 threads take 16 buckets each");
 // Lookahead distance of the tile order, in units of the near range: where a
 // unit's centre ray is this far out keys the unit. Grids beyond the Infinity
 // Cache key further out (their rays' working sets are what the order has to
@@ -126,6 +127,7 @@ static_assert(kTileW * kTileH == 64 && (1 << kTileWLog) == kTileW, "a tile is on
 int64_t tiles_per_env(int width, int height) {
     return (int64_t)((width + kQuadW - 1) / kQuadW) * ((height + kQuadH - 1) / kQuadH) * 4;
 }
+
 // Sorted tile-order blocks are dealt to the XCDs in chunks of this many
 // workgroups: XCD x takes chunks x, x+8, x+16, ... A chunk keeps one XCD's
 // concurrent rays in one part of the map, and interleaving the chunks
@@ -623,9 +625,18 @@ __global__ __launch_bounds__(256) void ray_setup(MarchArgs a, int sort_blocks) {
         }
     }
     __syncthreads();
-    // this block's first place in each bucket
-    for (int b = threadIdx.x; b < kOrderBuckets; b += blockDim.x)
-        if (h[b]) h[b] = atomicAdd(&a.order_hist[b], h[b]);
+    // this block's first place in each of the thread's 16 buckets: the
+    // atomics are independent, so all are issued before any result is
+    // awaited (one round trip to memory instead of 16 in a row)
+    constexpr int kBinsPer = kOrderBuckets / 256;
+    uint32_t cnt[kBinsPer], first[kBinsPer];
+#pragma unroll
+    for (int j = 0; j < kBinsPer; ++j) cnt[j] = h[threadIdx.x + j * 256];
+#pragma unroll
+    for (int j = 0; j < kBinsPer; ++j)
+        first[j] = cnt[j] ? atomicAdd(&a.order_hist[threadIdx.x + j * 256], cnt[j]) : 0u;
+#pragma unroll
+    for (int j = 0; j < kBinsPer; ++j) h[threadIdx.x + j * 256] = first[j];
     __syncthreads();
 #pragma unroll
     for (int j = 0; j < kPer; ++j) {
