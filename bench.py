@@ -19,11 +19,14 @@ from __future__ import annotations
 
 import argparse
 import json
+import math
 import os
 import statistics
 import sys
 import time
 from pathlib import Path
+
+import numpy as np
 
 ROOT = Path(__file__).resolve().parent
 for p in (str(ROOT), str(ROOT / "rl_cs1.6_surf_amd")):
@@ -354,6 +357,51 @@ def alg_bytes_per_load(store):
     return {"f32": 4.0, "f16": 2.0, "r16": 2.0 + 8.0 / 64.0}[store]
 
 
+def range_encoding(rng, near):
+    """The depth encoding of a ray that reached the range: the kernel's
+    fp32 sequence for t = range (t/near at or below near; above it
+    near/near + 0.25 * (1 - exp(-(t - near) / 2500)), the exponential
+    taken in fp64 and rounded once)."""
+    f = np.float32
+    t, nr = f(rng), f(near)
+    if not t > nr:
+        return float(t / nr)
+    xe = f(-(t - nr)) / f(2500.0)
+    ed = f(math.exp(float(xe)))
+    return float(nr / nr + f(0.25) * (f(1.0) - ed))
+
+
+def step_census(taps, out, w):
+    """The per-ray step statistics of the reference's step census
+    (tools/bench_lidar.py:188-215): grid loads per ray (mean, median, p90,
+    p99, max), the fraction of rays that exhaust the step budget and of rays
+    that reach the range (their encoding is the range's), the loop trips
+    that do work without an early exit (mean / max_steps); and, for this
+    kernel's early exit per tile of 16x4 rays, the fraction of a tile's lane
+    trips that do work (lane efficiency)."""
+    import torch
+    n = taps.shape[0]
+    flat = taps.reshape(-1)
+    srt = torch.sort(flat).values
+    q = [int(srt[min(srt.numel() - 1, int(f * srt.numel()))].item()) for f in (0.5, 0.9, 0.99)]
+    mean = float(flat.double().mean().item())
+    enc = out.reshape(n, w.height, w.width).float()
+    rng_enc = torch.tensor(range_encoding(w.range_units, w.near_range), dtype=torch.float32)
+    if out.dtype == torch.bfloat16:
+        rng_enc = rng_enc.to(torch.bfloat16).float()
+    reach = float((enc == rng_enc.to(enc.device)).double().mean().item())
+    eff = None
+    if w.height % 4 == 0 and w.width % 16 == 0:
+        tile_max = taps.view(n, w.height // 4, 4, w.width // 16, 16).amax(dim=(2, 4))
+        eff = round(float(flat.double().sum().item()) / (64.0 * float(tile_max.double().sum().item())), 4)
+    return {"loads_mean": round(mean, 3), "median": q[0], "p90": q[1], "p99": q[2],
+            "max": int(srt[-1].item()),
+            "exhaust_frac": round(float((flat >= w.max_steps).double().mean().item()), 5),
+            "reach_range_frac": round(reach, 5),
+            "work_frac_without_early_exit": round(mean / w.max_steps, 4),
+            "lane_efficiency_per_tile": eff}
+
+
 def measure_render(w, args, dev, *, graph, steps, warmup, out_shape=None, sc=None):
     """One workload: scene and poses, a lidar with the library defaults (or
     the command line's overrides), a census render (untimed) for the
@@ -391,11 +439,15 @@ def measure_render(w, args, dev, *, graph, steps, warmup, out_shape=None, sc=Non
     torch.cuda.synchronize()
     loads = int(taps.sum(dtype=torch.int64).item())
     max_taps = int(taps.max().item())
+    census = step_census(taps, out, w)
     del taps
     rays = n * w.width * w.height
     out_b = 2 if w.out_dtype == "bf16" else 4
     alg_bytes = int(loads * alg_bytes_per_load(w.store)) + rays * out_b + n * 24
-    _log(f"[bench] census: {loads} loads, mean {loads / rays:.2f}/ray, max {max_taps}")
+    _log(f"[bench] census: {loads} loads, mean {loads / rays:.2f}/ray, max {max_taps}; "
+         f"median {census['median']}, p90 {census['p90']}, p99 {census['p99']}, "
+         f"{census['exhaust_frac']:.2%} exhaust the budget, {census['reach_range_frac']:.2%} reach "
+         f"the range, lane efficiency {census['lane_efficiency_per_tile']}")
 
     step = lambda: lid.render(origin, yaw, pitch, duck, out=out)   # noqa: E731
     g = None
@@ -455,7 +507,7 @@ def measure_render(w, args, dev, *, graph, steps, warmup, out_shape=None, sc=Non
            "out": w.out_dtype, "out_shape": list(out.shape), "graph": bool(graph),
            "ms_per_step": ms_per_step, "launch_ms_median": statistics.median(launch_ms),
            "march_kernel_ms_avg": kernel_ms, "loads": loads, "alg_bytes": alg_bytes,
-           "rpl": lid.effective_rays_per_lane(n)}
+           "census": census, "rpl": lid.effective_rays_per_lane(n)}
     return res
 
 
@@ -474,11 +526,32 @@ def config_summary(r, traffic=None, traffic_src=None, limiter=None):
             "grid_loads_per_ray": round(r["loads"] / r["rays"], 4),
             "alg_bytes_per_launch": r["alg_bytes"],
             "alg_frac_of_hbm_peak": round(achieved / HBM_PEAK_GBS, 5),
+            "census": r.get("census"),
             "traffic_bytes_per_launch": traffic,
             "traffic_gbs": round(rate, 1) if rate else None,
             "traffic_source": traffic_src,
             "limiter": limiter.get("unit") if limiter else None,
             "rays_per_lane": r["rpl"]}
+
+
+def bench_steps_sweep(args, w, dev, shape):
+    """Render time against the step budget (tools/bench_lidar.py:149-156):
+    the workload timed at each budget of --steps-sweep, with its census."""
+    import dataclasses
+    import torch
+    sc = w.scene()
+    rows = []
+    for cap in [int(v) for v in args.steps_sweep.split(",")]:
+        r = measure_render(dataclasses.replace(w, max_steps=cap), args, dev, graph=args.graph,
+                           steps=args.steps, warmup=args.warmup, out_shape=shape, sc=sc)
+        r.pop("lid")
+        r.pop("sc")
+        rows.append({"max_steps": cap, "ms_per_batch": round(r["ms_per_step"], 5),
+                     "march_kernel_ms_avg": round(r["march_kernel_ms_avg"], 5),
+                     "g_rays_per_s": round(r["rays"] / (r["ms_per_step"] * 1e-3) / 1e9, 4),
+                     "census": r["census"]})
+        torch.cuda.empty_cache()
+    print(json.dumps({"workload": w.name, "steps_sweep": rows}), flush=True)
 
 
 # The other workloads of the metric, timed in the same run (GPU legs only):
@@ -521,6 +594,9 @@ def main(argv=None):
                     help="--goal: skip the reference's torch sweep loop")
     ap.add_argument("--graph", action="store_true",
                     help="capture one render in a hipGraph and time graph replays")
+    ap.add_argument("--steps-sweep", default=None,
+                    help="comma-separated step budgets: time the workload at each (the reference's "
+                         "render-ms-vs-MAX_STEPS sweep) and print one JSON line of them instead")
     args = ap.parse_args(argv)
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -537,6 +613,8 @@ def main(argv=None):
     if args.bake:
         return bench_bake(args, w, dev)
     shape = {n: s for n, _, s in OTHER_CONFIGS}.get(w.name)
+    if args.steps_sweep:
+        return bench_steps_sweep(args, w, dev, shape)
     r = measure_render(w, args, dev, graph=args.graph, steps=args.steps, warmup=args.warmup,
                        out_shape=shape)
     sc, lid = r.pop("sc"), r.pop("lid")
@@ -577,7 +655,8 @@ def main(argv=None):
                    "grid_loads_per_ray": round(r["loads"] / rays, 4),
                    "graph": bool(args.graph),
                    "launch_ms_median": round(r["launch_ms_median"], 5),
-                   "march_kernel_ms_avg": round(kernel_ms, 5)},
+                   "march_kernel_ms_avg": round(kernel_ms, 5),
+                   "census": r["census"]},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 5), "traffic": traffic,
                      "traffic_gbs": (round(traffic / (kernel_ms * 1e-3) / 1e9, 1)

@@ -7,6 +7,7 @@ import subprocess
 import sys
 from pathlib import Path
 
+import numpy as np
 import pytest
 
 ROOT = Path(__file__).resolve().parents[1]
@@ -95,3 +96,25 @@ def test_config_summary_carries_the_profiled_traffic_rate():
     stale = bench.config_summary(r)
     assert stale["traffic_bytes_per_launch"] is None and stale["traffic_gbs"] is None
     assert stale["limiter"] is None
+
+
+def test_range_encoding_is_the_kernels_encoding_of_the_range():
+    import oracle
+    for rng, near in ((6144.0, 2000.0), (1536.0, 1536.0), (23529.728600219765, 2000.0), (900.0, 400.0)):
+        assert bench.range_encoding(rng, near) == oracle.encode(float(np.float32(rng)), near)
+
+
+def test_step_census_statistics_on_a_known_tally():
+    import torch
+    from types import SimpleNamespace
+    w = SimpleNamespace(height=4, width=16, max_steps=10, range_units=100.0, near_range=100.0)
+    taps = torch.arange(1, 65, dtype=torch.int32).clamp(max=10).view(1, 4, 16)
+    out = torch.zeros(1, 4, 16)
+    out[0, 0, :3] = 1.0   # the range's encoding when near == range
+    c = bench.step_census(taps, out, w)
+    assert c["max"] == 10 and c["median"] == 10 and c["p90"] == 10
+    assert c["exhaust_frac"] == round(55 / 64, 5)
+    assert c["reach_range_frac"] == round(3 / 64, 5)
+    assert c["loads_mean"] == round((45 + 550) / 64, 3)
+    # one 16x4 tile whose slowest ray takes 10 steps
+    assert c["lane_efficiency_per_tile"] == round(595 / 640, 4)
