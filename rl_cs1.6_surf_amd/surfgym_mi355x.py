@@ -99,6 +99,9 @@ def _main(argv) -> int:
         return 2
     install()
     sys.argv = list(argv)
+    # as `python SCRIPT` would: the script's directory first on the path, in
+    # place of this file's (whose surfgym/ must not shadow the reference's)
+    sys.path[0] = str(Path(argv[0]).resolve().parent)
     runpy.run_path(argv[0], run_name="__main__")
     return 0
 
