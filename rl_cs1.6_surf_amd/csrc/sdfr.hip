@@ -23,13 +23,15 @@
 // are evaluated in fp64 and rounded once to fp32, which gives the correctly
 // rounded fp32 value except in cases rarer than 1 in 2^28.
 //
-// One render is two or three launches on the caller's stream:
+// One render is one to three launches on the caller's stream:
 //   1. ray_setup: per env, the (sin, cos) of its H row pitch angles and W
 //      column yaw angles, and its eye point — all the transcendental work of
 //      ray setup, (H+W) fp64 sincos per env instead of two per ray;
 //      With the lookahead tile order the same launch also keys the tiles by
 //      where they look and counts them into buckets, and order_scatter
-//      writes the sorted list (see "tile order");
+//      writes the sorted list (see "tile order"). A small unsorted render
+//      (under 8192 tiles, one ray per lane) skips this launch: each march
+//      wave builds the table entries of its own tile;
 //   2. the march, in one of two schedules with identical results:
 //      - tiles (default): launch-scheduled two-wave workgroups, each wave
 //        marching RPL 16x4 pixel tiles at once, RPL rays per lane (1 or 2,
@@ -143,6 +145,10 @@ constexpr uint32_t kNoVoxel = 0xffffffffu;
 // wave's instructions per step: 16-20% faster at 1-16 envs of 128x64, 5% at
 // 256; equal at 512, beyond which two tiles per wave win.
 constexpr int64_t kSmallRenderTiles = 1 << 16;
+#ifndef SDFR_INLINE_SETUP_TILES
+#define SDFR_INLINE_SETUP_TILES (1 << 13)
+#endif
+constexpr int64_t kInlineSetupTiles = SDFR_INLINE_SETUP_TILES;
 
 // ---------------------------------------------------------------- errors --
 thread_local char g_err[512];
@@ -368,6 +374,8 @@ struct MarchArgs {
     int order_shift;              // voxel index >> shift = tile-order cell
     float lookahead;              // distance along a unit's centre ray that keys it
     int rpl;                      // this render's rays per lane (tiles) or slots per wave
+    int inline_setup;             // tiles schedule, small unsorted render: each wave builds its
+                                  // tile's ray-table entries itself (no ray-setup launch)
     int order_unit;               // tiles per sorted unit: one workgroup's, kTileWaves * RPL
     int pack_off;                 // tiles schedule: word offset of the packing lane lists in LDS
     int64_t order_units;          // units the order sorts
@@ -764,14 +772,40 @@ __global__ __launch_bounds__(64 * kTileWaves) void march_tiles(MarchArgs a) {
         const int c = __builtin_amdgcn_readfirstlane(rc0.y) + (lane & (kTileW - 1));
         valid[j] = tile_ok && r < a.H && c < a.W;
         const int rr = min(r, a.H - 1), cc = min(c, a.W - 1);
-        const float2* rt = a.rt + (int64_t)n * a.rt_stride;
-        const float2 e01 = rt[a.H + a.W], e2 = rt[a.H + a.W + 1];
+        float2 row, col, e01, e2;
         float2 psc = make_float2(0.f, 0.f), ysc = make_float2(0.f, 0.f);
-        if constexpr (CAMERA == SDFR_CAM_PINHOLE) {
-            psc = rt[a.H + a.W + 2];
-            ysc = rt[a.H + a.W + 3];
+        if (RPL == 1 && a.inline_setup) {
+            // a small render: the wave builds the entries of the env's ray
+            // table its tile reads (the values the ray-setup launch would
+            // write, by the same function): lanes 0-3 the tile's rows, lanes
+            // 4-19 its columns, handed to every lane by ds_bpermute (all 64
+            // lanes are active here)
+            const int r0 = __builtin_amdgcn_readfirstlane(rc0.x);
+            const int c0 = __builtin_amdgcn_readfirstlane(rc0.y);
+            float2 mine = make_float2(0.f, 0.f);
+            if (lane < kTileH) mine = table_entry(a, n, min(r0 + lane, a.H - 1));
+            else if (lane < kTileH + kTileW) mine = table_entry(a, n, a.H + min(c0 + lane - kTileH, a.W - 1));
+            const int from_row = lane >> kTileWLog, from_col = kTileH + (lane & (kTileW - 1));
+            row = make_float2(lane_pull(from_row, mine.x), lane_pull(from_row, mine.y));
+            col = make_float2(lane_pull(from_col, mine.x), lane_pull(from_col, mine.y));
+            e01 = table_entry(a, n, a.H + a.W);
+            e2 = table_entry(a, n, a.H + a.W + 1);
+            if constexpr (CAMERA == SDFR_CAM_PINHOLE) {
+                psc = table_entry(a, n, a.H + a.W + 2);
+                ysc = table_entry(a, n, a.H + a.W + 3);
+            }
+        } else {
+            const float2* rt = a.rt + (int64_t)n * a.rt_stride;
+            row = rt[rr];
+            col = rt[a.H + cc];
+            e01 = rt[a.H + a.W];
+            e2 = rt[a.H + a.W + 1];
+            if constexpr (CAMERA == SDFR_CAM_PINHOLE) {
+                psc = rt[a.H + a.W + 2];
+                ysc = rt[a.H + a.W + 3];
+            }
         }
-        const float3 d = ray_dir<CAMERA>(rt[rr], rt[a.H + cc], psc, ysc);
+        const float3 d = ray_dir<CAMERA>(row, col, psc, ysc);
         ex[j] = e01.x;
         ey[j] = e01.y;
         ez[j] = e2.x;
@@ -817,6 +851,13 @@ __global__ __launch_bounds__(64 * kTileWaves) void march_tiles(MarchArgs a) {
     uint64_t live[RPL];
 #pragma unroll
     for (int j = 0; j < RPL; ++j) live[j] = __builtin_amdgcn_ballot_w64(alive[j]);
+    // Every set-up load lands before the loop, so the loop's waits count
+    // only its own gathers. With a set-up load still in flight at the loop's
+    // entry the compiler puts a full vmcnt(0) wait inside the loop, before
+    // the second tile's address math, and every step then waits for the
+    // first tile's gather before issuing the second's: the two gathers of a
+    // lane no longer overlap (ramp_field 0.480 -> 0.533 ms).
+    __builtin_amdgcn_s_waitcnt(0);
     for (int k = 1; k < a.max_steps; ++k) {
         uint64_t any = 0;
 #pragma unroll
@@ -1449,6 +1490,7 @@ int32_t render_impl(const char* fn, const SdfrGrid* grid, const SdfrCam* cam, co
     a.order_unit = kTileWaves * a.rpl;
     a.order_units = (a.total_tiles + a.order_unit - 1) / a.order_unit;
     a.logical_tiles = a.total_tiles;
+    a.inline_setup = 0;
     if (grid->tile_order == SDFR_ORDER_LOOKAHEAD && (grid->schedule == SDFR_SCHED_TILES || surf) &&
         a.total_tiles >= grid->order_min_tiles) {
         uint8_t* ws = (uint8_t*)workspace + ray_table_bytes(cam->width, cam->height, poses->n_envs);
@@ -1462,6 +1504,19 @@ int32_t render_impl(const char* fn, const SdfrGrid* grid, const SdfrCam* cam, co
         const int maxdim = max(a.nx, max(a.ny, a.nz));
         while (((maxdim - 1) >> a.order_shift) >= (1 << kOrderCellsLog)) ++a.order_shift;
     }
+
+    // A small unsorted tiles render builds its ray tables inside the march:
+    // the 20 table entries a tile reads cost its wave ~1-2 us of fp64 trig,
+    // less than the ray-setup launch and the gap before the march (~4 + 3 us;
+    // 1-16 envs render 8-13% faster). From ~64 envs on, the trig repeated
+    // in every tile costs more than the launch it saves, so larger renders
+    // share each env's table among its 128 tiles. Only the one-ray-per-lane
+    // march, the default below 65536 tiles, carries the inline path: the
+    // fp64 trig doubles a kernel's registers, which the two-ray march of
+    // large renders should not pay for.
+    if (!a.perm && (grid->schedule == SDFR_SCHED_TILES || surf) && a.total_tiles < kInlineSetupTiles &&
+        a.rpl == 1)
+        a.inline_setup = 1;
 
     // plan every launch before enqueueing any
     const bool census = image->taps != nullptr;
@@ -1490,12 +1545,14 @@ int32_t render_impl(const char* fn, const SdfrGrid* grid, const SdfrCam* cam, co
             return fail(-4, "%s: clearing the tile order's counts failed: %s", fn, hipGetErrorString(e));
         grid->hist_dirty = false;
     }
-    if (cam->camera == SDFR_CAM_PINHOLE)
-        ray_setup<SDFR_CAM_PINHOLE><<<(int)(table_blocks + sort_blocks), 256, 0, st>>>(a, (int)sort_blocks);
-    else
-        ray_setup<SDFR_CAM_EQUIANGULAR><<<(int)(table_blocks + sort_blocks), 256, 0, st>>>(a, (int)sort_blocks);
-    e = hipGetLastError();
-    if (e != hipSuccess) return fail(-4, "%s: ray setup launch failed: %s", fn, hipGetErrorString(e));
+    if (!a.inline_setup) {
+        if (cam->camera == SDFR_CAM_PINHOLE)
+            ray_setup<SDFR_CAM_PINHOLE><<<(int)(table_blocks + sort_blocks), 256, 0, st>>>(a, (int)sort_blocks);
+        else
+            ray_setup<SDFR_CAM_EQUIANGULAR><<<(int)(table_blocks + sort_blocks), 256, 0, st>>>(a, (int)sort_blocks);
+        e = hipGetLastError();
+        if (e != hipSuccess) return fail(-4, "%s: ray setup launch failed: %s", fn, hipGetErrorString(e));
+    }
     // from here on a sorted render has counted into order_hist
     auto abandon = [&](const char* what, hipError_t err) -> int32_t {
         if (a.order_hist) {

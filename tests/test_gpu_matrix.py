@@ -4,7 +4,10 @@ The render is a family of kernels: grid store (fp32, fp16, r16) x layout
 (bricks, the reference's linear order) x camera (equiangular, pinhole) x
 output (f32, bf16) x census (load counts on or off) x schedule (tiles with
 one or two tiles per wave, persistent) x tile order (launch, lookahead),
-plus the surf-mask channel. Each combination renders the same small scene on
+plus the surf-mask channel. One tile per wave in launch order is a small
+render's path, where each wave builds its tile's ray-table entries itself;
+the other schedules and the sorted order read the tables the ray-setup
+launch writes. Each combination renders the same small scene on
 an image that leaves quads of tiles partly outside it, and must equal the
 oracle on the grid as stored: depth encodings bit for bit (bf16: the oracle's
 fp32 encodings rounded to nearest even), per-ray load counts exactly.
