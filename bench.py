@@ -559,7 +559,8 @@ def bench_steps_sweep(args, w, dev, shape):
 OTHER_CONFIGS = (("small_ramps", False, None),
                  ("winding_track", False, None),
                  ("sparse_grazing", False, None),
-                 ("ramp_field_r16_bf16", True, lambda n: (n, 1, 64, 128)))
+                 ("ramp_field_r16_bf16", True, lambda n: (n, 1, 64, 128)),
+                 ("ramp_field_f16_bf16", True, lambda n: (n, 1, 64, 128)))
 
 
 def main(argv=None):

@@ -230,20 +230,26 @@ struct R16 {};
 template <typename GT>
 constexpr int kElemLog = std::is_same<GT, float>::value ? 2 : 1;   // log2 bytes per stored voxel
 
-// Slot packing of the tiles schedule (march_tiles) for 2-byte stores, where
-// a gather touches about half the lines of an fp32 one and vector issue is
-// the tighter bound.
+// Slot packing of the tiles schedule (march_tiles), on for r16 bricks,
+// where each sample is up to two gathers (code and brick header) and fewer
+// gather instructions pay: ramp_field_r16_bf16's march 2.266 ms with
+// packing, 2.365 without, 2.323 with packing and voxel reuse together. On
+// fp16 bricks voxel reuse without packing is faster (1.664 against
+// 1.712 ms), so fp16 does not pack unless built with SDFR_F16_PACK=1.
 #ifndef SDFR_R16_PACK
 #define SDFR_R16_PACK 1
 #endif
+#ifndef SDFR_F16_PACK
+#define SDFR_F16_PACK 0
+#endif
 // r16: a ray keeps the header of the brick it last sampled and gathers only
-// the code while it stays in that brick (ramp_field, 8192 envs, bf16 out:
-// 2.461 -> 2.381 ms with slot packing; without packing 2.482 / 2.432 ms).
+// the code while it stays in that brick (march 2.266 ms, 2.366 re-reading
+// the header at every code gather).
 #ifndef SDFR_R16_HDR_REUSE
 #define SDFR_R16_HDR_REUSE 1
 #endif
 template <typename GT>
-constexpr bool kPackStore = std::is_same<GT, __half>::value ||
+constexpr bool kPackStore = (std::is_same<GT, __half>::value && SDFR_F16_PACK) ||
                             (std::is_same<GT, R16>::value && SDFR_R16_PACK);
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
@@ -272,10 +278,14 @@ struct GridReader {
             return decode(code(off), h);
         }
     }
-    // r16 parts: the code at `off` and its brick's (base, scale)
+    // 2-byte stores: the 16-bit code at `off` (fp16 bits, or an r16 code)
     __device__ __forceinline__ uint32_t code(uint32_t off) const {
         return __builtin_amdgcn_raw_buffer_load_b16(codes, off, 0, 0);
     }
+    static __device__ __forceinline__ float from_code(uint32_t q) {   // fp16
+        return __half2float(__ushort_as_half((unsigned short)q));
+    }
+    // r16: its brick's (base, scale)
     __device__ __forceinline__ float2 header(uint32_t off) const {
         const auto bs = __builtin_amdgcn_raw_buffer_load_b64(hdr, (off >> 4) & ~7u, 0, 0);
         return make_float2(__uint_as_float(bs[0]), __uint_as_float(bs[1]));
@@ -717,7 +727,7 @@ __device__ __forceinline__ uint32_t lane_rank(uint64_t m) {   // set bits of m b
 // 0 to t. Step 0 needs no gather: every ray of an env samples the eye voxel
 // first, and the ray-table pass has read that value once per env.
 //
-// Slot packing (fp16 grids, RPL 2): once the live rays of a wave's two tiles
+// Slot packing (r16 grids, RPL 2): once the live rays of a wave's two tiles
 // fit in 64 lanes, the second tile's live rays move into the first tile's
 // ended lanes (ds_bpermute, lane lists in LDS) and the second slot stops
 // issuing address math and gathers. A ray's state travels with it, its
@@ -742,10 +752,11 @@ __global__ __launch_bounds__(64 * kTileWaves) void march_tiles(MarchArgs a) {
     const int64_t tile0 = ((int64_t)blk * kTileWaves + wave) * RPL;
     if (tile0 >= a.logical_tiles) return;
 
-    // Slot packing (below): on for fp16 grids, where a gather touches half as
-    // many lines and vector issue is the tighter bound; on fp32 grids the
-    // texture path binds and packing (rays of two tiles in one gather) costs
-    // ~3% more L1 tag accesses than the instructions it saves.
+    // Slot packing (below): on for r16 grids, whose samples take up to two
+    // gathers; on fp32 grids the texture path binds and packing (rays of
+    // two tiles in one gather) costs ~3% more L1 tag accesses than the
+    // instructions it saves, and on fp16 grids keeping voxel reuse instead
+    // is faster.
     constexpr bool kPack = RPL == 2 && !SURF && kPackStore<GT>;
     float ex[RPL], ey[RPL], ez[RPL], dx[RPL], dy[RPL], dz[RPL], t[RPL];
     int env[RPL], pix[RPL];   // env index and r*W + c of each ray (-1: no pixel)
@@ -835,13 +846,15 @@ __global__ __launch_bounds__(64 * kTileWaves) void march_tiles(MarchArgs a) {
     // on bookkeeping. A tile whose rays have all ended skips both.
     // offset and value of each ray's most recent gather (a march step that
     // stays in that voxel reads the value again without a gather). Off where
-    // slot packing is on: vector issue binds there, and the compare and the
-    // kept offset cost more than the gathers they save (~1%).
+    // slot packing is on: a packed slot mixes two tiles' rays, and reuse
+    // there measured slower (r16: 2.323 against 2.266 ms).
     constexpr bool kReuse = !kPack;
+    constexpr bool kRaw = !std::is_same<GT, float>::value;
     uint32_t last_off[RPL];
     float last_sd[RPL];
+    uint32_t last_raw[RPL];   // 2-byte stores: the code of the most recent gather
 #pragma unroll
-    for (int j = 0; j < RPL; ++j) { last_off[j] = kNoVoxel; last_sd[j] = 0.0f; }
+    for (int j = 0; j < RPL; ++j) { last_off[j] = kNoVoxel; last_sd[j] = 0.0f; last_raw[j] = 0u; }
     // r16 with header reuse: the brick (offset / 128) whose header each ray holds
     constexpr bool kHdrReuse = std::is_same<GT, R16>::value && SDFR_R16_HDR_REUSE;
     uint32_t hdr_brick[RPL];
@@ -921,15 +934,18 @@ __global__ __launch_bounds__(64 * kTileWaves) void march_tiles(MarchArgs a) {
                 // a step that stays in the voxel of the ray's previous sample
                 // reuses that value: same voxel, same sample, one line fewer
                 // for the texture path
-                if constexpr (kHdrReuse) {
-                    // the brick's header only when the ray enters another brick
+                if constexpr (kRaw) {
+                    // 2-byte stores keep the gathered code as it is (and
+                    // r16 its brick's header, read only when the ray
+                    // enters another brick); it is decoded below
                     if (!kReuse || off != last_off[j]) {
-                        const uint32_t q = rd.code(off);
-                        if ((off >> 7) != hdr_brick[j]) {
-                            hdr_val[j] = rd.header(off);
-                            hdr_brick[j] = off >> 7;
+                        last_raw[j] = rd.code(off);
+                        if constexpr (std::is_same<GT, R16>::value) {
+                            if (!kHdrReuse || (off >> 7) != hdr_brick[j]) {
+                                hdr_val[j] = rd.header(off);
+                                hdr_brick[j] = off >> 7;
+                            }
                         }
-                        last_sd[j] = GridReader<GT>::decode(q, hdr_val[j]);
                         last_off[j] = off;
                     }
                 } else if constexpr (!kReuse) {
@@ -938,6 +954,19 @@ __global__ __launch_bounds__(64 * kTileWaves) void march_tiles(MarchArgs a) {
                     last_sd[j] = rd(off);
                     last_off[j] = off;
                 }
+            }
+        }
+        // Decoding a 2-byte code right after its own gather would make the
+        // compiler wait for that gather before the next tile's address math,
+        // so the gathers of a lane's tiles would not overlap; the codes are
+        // decoded once every tile's gathers are issued.
+#pragma unroll
+        for (int j = 0; j < RPL; ++j) {
+            if constexpr (kRaw) {
+                if constexpr (std::is_same<GT, R16>::value)
+                    last_sd[j] = GridReader<GT>::decode(last_raw[j], hdr_val[j]);
+                else
+                    last_sd[j] = GridReader<GT>::from_code(last_raw[j]);
             }
             sd[j] = last_sd[j];
         }

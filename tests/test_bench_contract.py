@@ -57,7 +57,8 @@ def test_profiles_were_measured_on_the_current_kernels():
 @pytest.mark.parametrize("key", ["ramp_field tiles rpl=2 brick4 f32 order=lookahead",
                                  "winding_track tiles rpl=1 brick4 f32 order=lookahead",
                                  "sparse_grazing tiles rpl=2 brick4 f32 order=lookahead",
-                                 "ramp_field_r16_bf16 tiles rpl=2 brick4 r16 order=lookahead"])
+                                 "ramp_field_r16_bf16 tiles rpl=2 brick4 r16 order=lookahead",
+                                 "ramp_field_f16_bf16 tiles rpl=2 brick4 f16 order=lookahead"])
 def test_bench_workloads_have_profiled_traffic(key):
     traffic, _ = bench.profile_records()
     value, src = bench.profiled(key, traffic, "bytes")
@@ -66,7 +67,7 @@ def test_bench_workloads_have_profiled_traffic(key):
 
 
 @pytest.mark.parametrize("name", ["ramp_field", "winding_track", "sparse_grazing",
-                                  "ramp_field_r16_bf16", "small_ramps"])
+                                  "ramp_field_r16_bf16", "ramp_field_f16_bf16", "small_ramps"])
 def test_bench_workloads_have_a_measured_limiter(name):
     _, limiter = bench.profile_records()
     value, src = bench.profiled(name, limiter)
@@ -76,11 +77,13 @@ def test_bench_workloads_have_a_measured_limiter(name):
 
 def test_other_configurations_cover_the_metric_workloads():
     names = {n for n, _, _ in bench.OTHER_CONFIGS}
-    assert names == {"small_ramps", "winding_track", "sparse_grazing", "ramp_field_r16_bf16"}
+    assert names == {"small_ramps", "winding_track", "sparse_grazing", "ramp_field_r16_bf16",
+                     "ramp_field_f16_bf16"}
     graph = {n: g for n, g, _ in bench.OTHER_CONFIGS}
-    assert graph["ramp_field_r16_bf16"] is True
-    shape = {n: s for n, _, s in bench.OTHER_CONFIGS}["ramp_field_r16_bf16"]
-    assert shape(8192) == (8192, 1, 64, 128)
+    shape = {n: s for n, _, s in bench.OTHER_CONFIGS}
+    for fused in ("ramp_field_r16_bf16", "ramp_field_f16_bf16"):
+        assert graph[fused] is True
+        assert shape[fused](8192) == (8192, 1, 64, 128)
 
 
 def test_config_summary_carries_the_profiled_traffic_rate():
