@@ -356,6 +356,8 @@ struct MarchArgs {
     int store;                    // SDFR_F32 | SDFR_F16 | SDFR_R16
     float fnx1, fny1, fnz1;       // n-1 as float: the clamp bound
     float mnx, mny, mnz, inv_cell;
+    float smx, smy, smz;          // -mins * inv_cell, exact when pow2_cell
+    int pow2_cell;                // inv_cell is a power of two and mins * inv_cell exact
     float rng, near, hit_eps, min_step;
     int max_steps;
     int W, H, camera;
@@ -510,6 +512,26 @@ template <int OUT_DTYPE>
 __device__ __forceinline__ void store_enc(void* out, int64_t o, float enc) {
     if constexpr (OUT_DTYPE == SDFR_BF16) ((uint16_t*)out)[o] = f32_to_bf16_rne(enc);
     else ((float*)out)[o] = enc;
+}
+
+// A sample's coordinate in voxel units along one axis, (p - mins) * inv_cell
+// in the reference's two roundings (vision.py:104-106). When inv_cell is a
+// power of two the scaling is exact, so round(p - mins) * inv_cell equals
+// round((p - mins) * inv_cell), which one fma computes from p and the exact
+// product -mins * inv_cell (sm): the same bits, one instruction fewer (any
+// result below the normal range truncates to voxel 0 either way).
+// A vector instruction reads at most one scalar register, so the fma's two
+// per-render constants cannot both stay scalar: inv_cell is handed to the
+// loop as a per-lane value (x + 0 * lane, which is x exactly and which the
+// compiler must keep in a vector register) and sm stays scalar.
+__device__ __forceinline__ float in_vgpr(float x) {
+    return x + 0.0f * (float)(threadIdx.x & 63);
+}
+
+template <bool POW2>
+__device__ __forceinline__ float voxel_coord(float p, float mins, float sm, float inv_cell) {
+    if constexpr (POW2) return __builtin_fmaf(p, inv_cell, sm);
+    else return (p - mins) * inv_cell;
 }
 
 // One march step of a live ray (vision.py:101-111). Returns whether the ray
@@ -871,6 +893,11 @@ __global__ __launch_bounds__(64 * kTileWaves) void march_tiles(MarchArgs a) {
     // first tile's gather before issuing the second's: the two gathers of a
     // lane no longer overlap (ramp_field 0.480 -> 0.533 ms).
     __builtin_amdgcn_s_waitcnt(0);
+    // The loop, once per form of the voxel index (see voxel_coord): with a
+    // power-of-two cell the subtract and the scaling are one fma.
+    const float ic_v = in_vgpr(a.inv_cell);
+    auto march = [&](auto pow2_cell) {
+    constexpr bool kPow2 = decltype(pow2_cell)::value;
     for (int k = 1; k < a.max_steps; ++k) {
         uint64_t any = 0;
 #pragma unroll
@@ -927,9 +954,10 @@ __global__ __launch_bounds__(64 * kTileWaves) void march_tiles(MarchArgs a) {
                 const float px = ex[j] + dx[j] * t[j];
                 const float py = ey[j] + dy[j] * t[j];
                 const float pz = ez[j] + dz[j] * t[j];
-                const int ix = (int)__builtin_amdgcn_fmed3f((px - a.mnx) * a.inv_cell, 0.0f, a.fnx1);
-                const int iy = (int)__builtin_amdgcn_fmed3f((py - a.mny) * a.inv_cell, 0.0f, a.fny1);
-                const int iz = (int)__builtin_amdgcn_fmed3f((pz - a.mnz) * a.inv_cell, 0.0f, a.fnz1);
+                const float ic = kPow2 ? ic_v : a.inv_cell;
+                const int ix = (int)__builtin_amdgcn_fmed3f(voxel_coord<kPow2>(px, a.mnx, a.smx, ic), 0.0f, a.fnx1);
+                const int iy = (int)__builtin_amdgcn_fmed3f(voxel_coord<kPow2>(py, a.mny, a.smy, ic), 0.0f, a.fny1);
+                const int iz = (int)__builtin_amdgcn_fmed3f(voxel_coord<kPow2>(pz, a.mnz, a.smz, ic), 0.0f, a.fnz1);
                 const uint32_t off = tab[ix] + tab[a.nx + iy] + tab[a.nx + a.ny + iz];
                 // a step that stays in the voxel of the ray's previous sample
                 // reuses that value: same voxel, same sample, one line fewer
@@ -981,6 +1009,9 @@ __global__ __launch_bounds__(64 * kTileWaves) void march_tiles(MarchArgs a) {
             t[j] = __builtin_amdgcn_inverse_ballot_w64(live[j]) ? tn : t[j];
         }
     }
+    };
+    if (a.pow2_cell) march(std::true_type{});
+    else march(std::false_type{});
     constexpr int CH = SURF ? 2 : 1;
 #pragma unroll
     for (int j = 0; j < RPL; ++j) {
@@ -1460,6 +1491,22 @@ void set_grid_args(MarchArgs* a, const SdfrGrid* grid) {
     a->mny = grid->desc.mins[1];
     a->mnz = grid->desc.mins[2];
     a->inv_cell = (float)(1.0 / (double)grid->desc.cell);   // Python's 1.0/cell, then fp32
+    // -mins * inv_cell for the fma form of the voxel index, used when both
+    // that product and inv_cell are exact (inv_cell a power of two)
+    int e2 = 0;
+    const bool pow2 = frexp((double)a->inv_cell, &e2) == 0.5;
+    const double m[3] = {a->mnx, a->mny, a->mnz};
+    float sm[3];
+    bool exact = pow2;
+    for (int i = 0; i < 3; ++i) {
+        const double prod = -m[i] * (double)a->inv_cell;
+        sm[i] = (float)prod;
+        exact = exact && (double)sm[i] == prod && (prod == 0.0 || fabs(prod) >= 0x1p-126);
+    }
+    a->smx = sm[0];
+    a->smy = sm[1];
+    a->smz = sm[2];
+    a->pow2_cell = exact ? 1 : 0;
 }
 
 // The render behind sdfr_render. Everything that can be refused is checked
