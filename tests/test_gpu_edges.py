@@ -1,7 +1,8 @@
 """GPU edge cases of the render against the oracle: degenerate grid shapes
 (one voxel thick along any axis, a single voxel, partial bricks) in every
-store and layout, and eyes outside the grid on every side (every sample then
-reads the clamped border voxel first, vision.py:644-646)."""
+store and layout, eyes outside the grid on every side (every sample then
+reads the clamped border voxel first, vision.py:644-646), and grids whose
+cell or origin keeps the voxel index in subtract-then-scale form."""
 from __future__ import annotations
 
 import numpy as np
@@ -77,6 +78,35 @@ def test_eyes_outside_the_grid(dev, gdt, store, layout):
     got = lid.render(*[torch.as_tensor(a, device=dev) for a in (o, yaw, pitch, duck)])
     want, _ = oracle.render(g, np.full(3, -8.0), 16.0, o, yaw, pitch, duck, store=store, **kw)
     assert np.array_equal(got.cpu().numpy(), want)
+
+
+@pytest.mark.parametrize("cell,mins", [(12.0, (-8.0, -8.0, -8.0)), (24.0, (3.0, -5.0, 0.0)),
+                                       (16.0, (1e-40, -8.0, 2.5))])
+@pytest.mark.parametrize("gdt,store,layout", _STORES)
+def test_grids_without_the_single_rounding_index(dev, cell, mins, gdt, store, layout):
+    """The march forms a sample's voxel coordinate as one fma when inv_cell
+    is a power of two and mins * inv_cell is exact, and as the reference's
+    subtract-then-scale otherwise (vision.py:104-106). Cells of 12 and 24 u,
+    and a 16 u cell whose x origin is subnormal (so its scaled value is not
+    exact), take the second form: one and two rays per lane, both tile
+    orders, against the oracle."""
+    shape = (9, 14, 17)
+    g = _field(shape, 5)
+    mins = np.array(mins, np.float32)
+    n = 12
+    o, yaw, pitch, duck = _poses(shape, n, 13)
+    kw = dict(width=40, height=12, range_units=1200.0, near_range=500.0, max_steps=64)
+    want, _ = oracle.render(g, mins, cell, o, yaw, pitch, duck, store=store, **kw)
+    lid = vision.GpuLidar.from_grid(g, mins, cell, grid_dtype=gdt, layout=layout, device=dev, **kw)
+    args = [torch.as_tensor(a, device=dev) for a in (o, yaw, pitch, duck)]
+    for rpl in (1, 2):
+        lid.set_schedule("tiles", rays_per_lane=rpl)
+        for order in ("launch", "lookahead"):
+            lid.set_tile_order(order, min_tiles=0)
+            print(f"case edges cell={cell} mins={mins.tolist()} store={store} layout={layout} "
+                  f"rpl={rpl} order={order}", flush=True)
+            got = lid.render(*args)
+            assert np.array_equal(got.cpu().numpy(), want), (cell, rpl, order)
 
 
 def test_the_largest_batch_renders_every_env(dev):
