@@ -34,7 +34,7 @@ extern "C" {
 
 /* Bumped on every struct or semantic change; the binding refuses a library
  * reporting another value. */
-#define SDFR_ABI_VERSION 12
+#define SDFR_ABI_VERSION 13
 
 /* Element types of caller arrays. */
 enum {
@@ -77,6 +77,14 @@ enum {
                                  units out (Morton order of coarse cells), so each XCD's L2
                                  serves rays looking at one part of the map; applied to
                                  renders of at least min_tiles tiles */
+};
+
+/* When the one-ray march reads border voxels from the grid's face copies
+ * (f32/f16 bricks keep each of the six border layers again as a 2D copy). */
+enum {
+    SDFR_FACES_AUTO = 0,  /* default: for grids beyond the Infinity Cache (above 192 MiB) */
+    SDFR_FACES_ON = 1,    /* whenever the march runs one ray per lane */
+    SDFR_FACES_OFF = 2    /* never */
 };
 
 /* Grid geometry: the reference's single grid definition, grid_dims()
@@ -189,6 +197,17 @@ SDFR_API int32_t sdfr_render_rays_per_lane(const SdfrGrid* grid, const SdfrCam* 
  * Synchronous; 0 or < 0. No reference counterpart. */
 SDFR_API int32_t sdfr_grid_set_tile_order(SdfrGrid* grid, int32_t order, int64_t min_tiles);
 
+/* Chooses when later renders on this handle read border voxels from the
+ * face copies (SDFR_FACES_*, default SDFR_FACES_AUTO). A sample outside the
+ * grid clamps to a border voxel (vision.py:104-106); on open scenes that is
+ * 37-42% of all samples, and a face copy keeps a border layer's voxels 32
+ * (fp32) or 64 (fp16) to a 128-byte line where the bricks hold 4-16. Only
+ * the one-ray-per-lane march reads them; the copies hold the bricks'
+ * values, so results do not depend on the mode. -3 for SDFR_FACES_ON on a
+ * grid without copies (r16, or the linear layout). Synchronous; 0 or < 0.
+ * No reference counterpart. */
+SDFR_API int32_t sdfr_grid_set_border_faces(SdfrGrid* grid, int32_t mode);
+
 /* Measurement hook, no reference counterpart: with a pair of the caller's
  * HIP events set (hipEvent_t, both or neither), every later render on this
  * handle records `start` on its stream right before the march kernel and
@@ -198,7 +217,7 @@ SDFR_API int32_t sdfr_grid_set_tile_order(SdfrGrid* grid, int32_t order, int64_t
 SDFR_API int32_t sdfr_grid_set_march_events(SdfrGrid* grid, void* start, void* stop);
 
 /* Bytes of device memory the handle's grid copy occupies (r16: codes and
- * brick headers). */
+ * brick headers; f32/f16 bricks: the bricks and the face copies). */
 SDFR_API int64_t sdfr_grid_bytes(const SdfrGrid* grid);
 
 /* Device bytes of the workspace sdfr_render needs for n_envs envs of this

@@ -173,6 +173,13 @@ struct SdfrGrid {
     int64_t bytes;         // all of it (r16: codes, padding and brick headers)
     int64_t code_bytes;    // the voxel values (r16: the uint16 codes), from offset 0
     int64_t hdr_off;       // r16: byte offset of the brick headers (float2 per brick), else 0
+    int64_t store_bytes;   // the voxel store alone (codes and r16 headers): what the
+                           // cache-residence rules look at
+    bool has_faces;        // f32/f16 bricks: border faces copied after the bricks
+    uint32_t face_off[3];  // byte offset of the z, y and x face pairs (low face first)
+    uint32_t face_bytes[3];// bytes of one face of each pair
+    int face_lines[2];     // face lines along x (z and y faces) and along y (x faces)
+    int32_t border_faces;  // SDFR_FACES_*: when the one-ray march reads them
     uint32_t* counters;    // persistent schedule: tile claim counters + exit counter
     int32_t schedule;      // SDFR_SCHED_*
     int32_t refill_lanes;  // persistent schedule: refill when this many lanes are free
@@ -388,6 +395,11 @@ struct MarchArgs {
     int rpl;                      // this render's rays per lane (tiles) or slots per wave
     int inline_setup;             // tiles schedule, small unsorted render: each wave builds its
                                   // tile's ray-table entries itself (no ray-setup launch)
+    int faces;                    // one-ray march: border voxels read from the face copies
+    int face_alog;                // log2 voxels per row of a face line (3 fp32, 4 fp16)
+    int face_lines_x, face_lines_y;
+    uint32_t face_off_z, face_off_y, face_off_x;        // low face of each pair
+    uint32_t face_bytes_z, face_bytes_y, face_bytes_x;  // one face of each pair
     int order_unit;               // tiles per sorted unit: one workgroup's, kTileWaves * RPL
     int pack_off;                 // tiles schedule: word offset of the packing lane lists in LDS
     int64_t order_units;          // units the order sorts
@@ -532,6 +544,38 @@ template <bool POW2>
 __device__ __forceinline__ float voxel_coord(float p, float mins, float sm, float inv_cell) {
     if constexpr (POW2) return __builtin_fmaf(p, inv_cell, sm);
     else return (p - mins) * inv_cell;
+}
+
+// Border faces. Samples outside the grid clamp to a border voxel
+// (vision.py:104-106): on the open synthetic scenes 37-42% of all gathers.
+// In 4x4x4 bricks a face's voxels are spread one or two per 64-byte sector
+// over the bricks along it, so f32/f16 grids also keep each of the six
+// border layers as a 2D copy after the bricks: lines of 128 bytes holding
+// 4 rows of 32 bytes (8 fp32 or 16 fp16 voxels) of the face's first axis,
+// the lines numbered first-axis-fastest. A voxel on several faces is read
+// from the z face, then the y face, then the x face; the copies hold the
+// same values, so the choice never changes a result. Face (A, B) of a pair:
+// z faces A = ix, B = iy; y faces A = ix, B = iz; x faces A = iy, B = iz.
+// Returns the face copy's byte offset of a border voxel, `off` otherwise.
+__device__ __forceinline__ uint32_t border_offset(const MarchArgs& a, int ix, int iy, int iz,
+                                                  uint32_t off) {
+    int A, B, lines;
+    uint32_t base;
+    if (iz == 0 || iz == a.nz - 1) {
+        A = ix; B = iy; lines = a.face_lines_x;
+        base = a.face_off_z + (iz != 0 ? a.face_bytes_z : 0u);
+    } else if (iy == 0 || iy == a.ny - 1) {
+        A = ix; B = iz; lines = a.face_lines_x;
+        base = a.face_off_y + (iy != 0 ? a.face_bytes_y : 0u);
+    } else if (ix == 0 || ix == a.nx - 1) {
+        A = iy; B = iz; lines = a.face_lines_y;
+        base = a.face_off_x + (ix != 0 ? a.face_bytes_x : 0u);
+    } else {
+        return off;
+    }
+    const int row = (1 << a.face_alog) - 1;
+    return base + (uint32_t)(((B >> 2) * lines + (A >> a.face_alog)) * 128 + (B & 3) * 32 +
+                             ((A & row) << (5 - a.face_alog)));
 }
 
 // One march step of a live ray (vision.py:101-111). Returns whether the ray
@@ -893,11 +937,13 @@ __global__ __launch_bounds__(64 * kTileWaves) void march_tiles(MarchArgs a) {
     // first tile's gather before issuing the second's: the two gathers of a
     // lane no longer overlap (ramp_field 0.480 -> 0.533 ms).
     __builtin_amdgcn_s_waitcnt(0);
-    // The loop, once per form of the voxel index (see voxel_coord): with a
-    // power-of-two cell the subtract and the scaling are one fma.
+    // The loop, once per form of the voxel index (see voxel_coord: with a
+    // power-of-two cell the subtract and the scaling are one fma) and, in the
+    // one-ray march, with and without the border face copies.
     const float ic_v = in_vgpr(a.inv_cell);
-    auto march = [&](auto pow2_cell) {
+    auto march = [&](auto pow2_cell, auto border_faces) {
     constexpr bool kPow2 = decltype(pow2_cell)::value;
+    constexpr bool kFaces = decltype(border_faces)::value;
     for (int k = 1; k < a.max_steps; ++k) {
         uint64_t any = 0;
 #pragma unroll
@@ -959,6 +1005,11 @@ __global__ __launch_bounds__(64 * kTileWaves) void march_tiles(MarchArgs a) {
                 const int iy = (int)__builtin_amdgcn_fmed3f(voxel_coord<kPow2>(py, a.mny, a.smy, ic), 0.0f, a.fny1);
                 const int iz = (int)__builtin_amdgcn_fmed3f(voxel_coord<kPow2>(pz, a.mnz, a.smz, ic), 0.0f, a.fnz1);
                 const uint32_t off = tab[ix] + tab[a.nx + iy] + tab[a.nx + a.ny + iz];
+                // where the value is read: the brick, or for a border voxel
+                // of a one-ray march on a grid beyond the Infinity Cache its
+                // face copy (see border_offset); `off` stays the voxel's name
+                uint32_t at = off;
+                if constexpr (kFaces) at = border_offset(a, ix, iy, iz, off);
                 // a step that stays in the voxel of the ray's previous sample
                 // reuses that value: same voxel, same sample, one line fewer
                 // for the texture path
@@ -967,7 +1018,7 @@ __global__ __launch_bounds__(64 * kTileWaves) void march_tiles(MarchArgs a) {
                     // r16 its brick's header, read only when the ray
                     // enters another brick); it is decoded below
                     if (!kReuse || off != last_off[j]) {
-                        last_raw[j] = rd.code(off);
+                        last_raw[j] = rd.code(at);
                         if constexpr (std::is_same<GT, R16>::value) {
                             if (!kHdrReuse || (off >> 7) != hdr_brick[j]) {
                                 hdr_val[j] = rd.header(off);
@@ -977,9 +1028,9 @@ __global__ __launch_bounds__(64 * kTileWaves) void march_tiles(MarchArgs a) {
                         last_off[j] = off;
                     }
                 } else if constexpr (!kReuse) {
-                    last_sd[j] = rd(off);
+                    last_sd[j] = rd(at);
                 } else if (off != last_off[j]) {
-                    last_sd[j] = rd(off);
+                    last_sd[j] = rd(at);
                     last_off[j] = off;
                 }
             }
@@ -1010,8 +1061,18 @@ __global__ __launch_bounds__(64 * kTileWaves) void march_tiles(MarchArgs a) {
         }
     }
     };
-    if (a.pow2_cell) march(std::true_type{});
-    else march(std::false_type{});
+    // each form of the loop is chosen once per wave, not tested per step:
+    // a per-step branch on the face flag alone cost small renders 3-6%
+    auto with_faces = [&](auto pow2_cell) {
+        if constexpr (RPL == 1) {
+            if (a.faces) march(pow2_cell, std::true_type{});
+            else march(pow2_cell, std::false_type{});
+        } else {
+            march(pow2_cell, std::false_type{});
+        }
+    };
+    if (a.pow2_cell) with_faces(std::true_type{});
+    else with_faces(std::false_type{});
     constexpr int CH = SURF ? 2 : 1;
 #pragma unroll
     for (int j = 0; j < RPL; ++j) {
@@ -1313,7 +1374,7 @@ size_t axis_lds_bytes(const MarchArgs& a) {
 // flight, fewer misses) and for small renders, else 2.
 int render_rpl(const SdfrGrid* g, int64_t tiles) {
     if (g->rays_per_lane > 0) return g->rays_per_lane;
-    return (g->bytes > kCacheResidentBytes || tiles < kSmallRenderTiles) ? 1 : 2;
+    return (g->store_bytes > kCacheResidentBytes || tiles < kSmallRenderTiles) ? 1 : 2;
 }
 
 // One march launch, chosen and sized before anything is enqueued, so that a
@@ -1329,7 +1390,7 @@ struct MarchPlan {
 template <typename GT, int LAYOUT, int OUT, int CAMERA, bool CENSUS, bool SURF>
 MarchPlan plan_tiles(MarchArgs& a, const SdfrGrid* g) {
     size_t lds = axis_lds_bytes(a);
-    if (g->bytes > kCacheResidentBytes && g->lds_per_cu > 0)
+    if (g->store_bytes > kCacheResidentBytes && g->lds_per_cu > 0)
         lds = max(lds, (size_t)g->lds_per_cu / kSpillBlocksPerCU);   // cap the workgroups per CU
     const int per_block = kTileWaves * a.rpl;
     const int64_t blocks = (a.logical_tiles + per_block - 1) / per_block;
@@ -1476,7 +1537,7 @@ void set_grid_args(MarchArgs* a, const SdfrGrid* grid) {
     a->code_bytes = (uint32_t)grid->code_bytes;
     const bool r16 = grid->store_dtype == SDFR_R16;
     a->hdr_off = r16 ? (uint32_t)grid->hdr_off : 0u;
-    a->hdr_bytes = r16 ? (uint32_t)(grid->bytes - grid->hdr_off) : 0u;
+    a->hdr_bytes = r16 ? (uint32_t)(grid->store_bytes - grid->hdr_off) : 0u;
     a->store = grid->store_dtype;
     a->nx = grid->desc.nx;
     a->ny = grid->desc.ny;
@@ -1560,13 +1621,25 @@ int32_t render_impl(const char* fn, const SdfrGrid* grid, const SdfrCam* cam, co
     a.order_key = nullptr;
     a.order_rank = nullptr;
     a.order_shift = 0;
-    a.lookahead = (grid->bytes > kCacheResidentBytes ? kOrderLookaheadSpilled : kOrderLookahead) *
+    a.lookahead = (grid->store_bytes > kCacheResidentBytes ? kOrderLookaheadSpilled : kOrderLookahead) *
                   cam->near;
     a.rpl = render_rpl(grid, a.total_tiles);
     a.order_unit = kTileWaves * a.rpl;
     a.order_units = (a.total_tiles + a.order_unit - 1) / a.order_unit;
     a.logical_tiles = a.total_tiles;
     a.inline_setup = 0;
+    a.faces = grid->has_faces &&
+              (grid->border_faces == SDFR_FACES_ON ||
+               (grid->border_faces == SDFR_FACES_AUTO && grid->store_bytes > kCacheResidentBytes));
+    a.face_alog = grid->store_dtype == SDFR_F32 ? 3 : 4;
+    a.face_lines_x = grid->face_lines[0];
+    a.face_lines_y = grid->face_lines[1];
+    a.face_off_z = grid->face_off[0];
+    a.face_off_y = grid->face_off[1];
+    a.face_off_x = grid->face_off[2];
+    a.face_bytes_z = grid->face_bytes[0];
+    a.face_bytes_y = grid->face_bytes[1];
+    a.face_bytes_x = grid->face_bytes[2];
     if (grid->tile_order == SDFR_ORDER_LOOKAHEAD && (grid->schedule == SDFR_SCHED_TILES || surf) &&
         a.total_tiles >= grid->order_min_tiles) {
         uint8_t* ws = (uint8_t*)workspace + ray_table_bytes(cam->width, cam->height, poses->n_envs);
@@ -1696,6 +1769,51 @@ int32_t scratch_for_current_device(const char* fn, const SdfrGrid* grid, void** 
 }  // namespace
 
 // ================================================================ C ABI ==
+// Copies the six border layers of the source grid into the face copies
+// (see border_offset), converting as relayout_grid does, so a face voxel
+// holds exactly its brick's value. One thread per face-copy element; rows
+// past the face's edge (a line's tail) hold 0 and are never addressed.
+template <typename ST, typename DT>
+__global__ __launch_bounds__(256) void fill_faces(const ST* __restrict__ src, DT* __restrict__ dst,
+                                                  int nx, int ny, int nz, int pair, int high,
+                                                  int lines, int64_t count) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= count) return;
+    constexpr int kRow = 32 / (int)sizeof(DT);                  // voxels per 32-byte row
+    constexpr int kLine = 4 * kRow;                             // voxels per 128-byte line
+    const int64_t line = i / kLine;
+    const int in = (int)(i - line * kLine);
+    const int A = (int)(line % lines) * kRow + in % kRow;
+    const int B = (int)(line / lines) * 4 + in / kRow;
+    int ix, iy, iz, na, nb;
+    if (pair == 0) { ix = A; iy = B; iz = high ? nz - 1 : 0; na = nx; nb = ny; }
+    else if (pair == 1) { ix = A; iz = B; iy = high ? ny - 1 : 0; na = nx; nb = nz; }
+    else { iy = A; iz = B; ix = high ? nx - 1 : 0; na = ny; nb = nz; }
+    float v = 0.0f;
+    if (A < na && B < nb) {
+        const int64_t s = ((int64_t)iz * ny + iy) * nx + ix;
+        if constexpr (sizeof(ST) == 2) v = __half2float(((const __half*)src)[s]);
+        else v = ((const float*)src)[s];
+    }
+    if constexpr (sizeof(DT) == 2) ((__half*)dst)[i] = __float2half_rn(v);
+    else ((float*)dst)[i] = v;
+}
+
+template <typename ST, typename DT>
+hipError_t launch_fill_faces(const void* src, SdfrGrid* g, hipStream_t st) {
+    for (int f = 0; f < 6; ++f) {
+        const int pair = f / 2;
+        const int64_t count = g->face_bytes[pair] / (int64_t)sizeof(DT);
+        DT* dst = (DT*)((char*)g->data + g->face_off[pair] + (f & 1) * (int64_t)g->face_bytes[pair]);
+        fill_faces<ST, DT><<<(int)((count + 255) / 256), 256, 0, st>>>(
+            (const ST*)src, dst, g->desc.nx, g->desc.ny, g->desc.nz, pair, f & 1,
+            g->face_lines[pair == 2 ? 1 : 0], count);
+        const hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+    }
+    return hipSuccess;
+}
+
 extern "C" {
 
 SDFR_API int32_t sdfr_abi_version(void) { return SDFR_ABI_VERSION; }
@@ -1766,8 +1884,24 @@ SDFR_API SdfrGrid* sdfr_grid_create(const SdfrGridDesc* desc, const void* src, i
     const int64_t code_bytes = count * elem;
     const int64_t n_bricks = count / 64;
     const int64_t hdr_off = store_dtype == SDFR_R16 ? align256(code_bytes) : 0;
-    const int64_t total_bytes =
+    const int64_t store_bytes =
         store_dtype == SDFR_R16 ? hdr_off + n_bricks * (int64_t)sizeof(float2) : code_bytes;
+    // f32/f16 bricks: the six border layers again, as 2D face copies after
+    // the bricks (border_offset), within the same buffer descriptor
+    const bool faces = store_dtype != SDFR_R16 && layout == SDFR_LAYOUT_BRICK4;
+    const int row = 32 / (int)elem;   // voxels per 32-byte row of a face line
+    const int lines_x = (desc->nx + row - 1) / row, lines_y = (desc->ny + row - 1) / row;
+    const int64_t face_bytes[3] = {(int64_t)lines_x * ((desc->ny + 3) / 4) * 128,
+                                   (int64_t)lines_x * ((desc->nz + 3) / 4) * 128,
+                                   (int64_t)lines_y * ((desc->nz + 3) / 4) * 128};
+    int64_t face_off[3] = {0, 0, 0};
+    int64_t total_bytes = store_bytes;
+    if (faces) {
+        face_off[0] = align256(store_bytes);
+        face_off[1] = face_off[0] + 2 * face_bytes[0];
+        face_off[2] = face_off[1] + 2 * face_bytes[1];
+        total_bytes = face_off[2] + 2 * face_bytes[2];
+    }
     if (total_bytes > (int64_t)0xffffffffLL ||
         (int64_t)desc->nx + desc->ny + desc->nz > kMaxAxisEntries) {
         fail(-2, "sdfr_grid_create: grid too large (%d x %d x %d, %lld bytes; limits: 4 GiB and "
@@ -1786,8 +1920,18 @@ SDFR_API SdfrGrid* sdfr_grid_create(const SdfrGridDesc* desc, const void* src, i
     g->by = by;
     g->bz = bz;
     g->bytes = total_bytes;
-    g->code_bytes = code_bytes;
+    g->store_bytes = store_bytes;
+    // the buffer descriptor of the voxel reads spans the face copies too
+    g->code_bytes = faces ? total_bytes : code_bytes;
     g->hdr_off = hdr_off;
+    g->has_faces = faces;
+    for (int i = 0; i < 3; ++i) {
+        g->face_off[i] = (uint32_t)face_off[i];
+        g->face_bytes[i] = faces ? (uint32_t)face_bytes[i] : 0u;
+    }
+    g->face_lines[0] = lines_x;
+    g->face_lines[1] = lines_y;
+    g->border_faces = SDFR_FACES_AUTO;
     g->data = nullptr;
     g->counters = nullptr;
     g->nz_data = nullptr;
@@ -1849,6 +1993,16 @@ SDFR_API SdfrGrid* sdfr_grid_create(const SdfrGridDesc* desc, const void* src, i
             e = launch_relayout<__half, float>(dsrc, g->data, g, count, st);
         else
             e = launch_relayout<__half, __half>(dsrc, g->data, g, count, st);
+    }
+    if (e == hipSuccess && faces) {
+        if (src_dtype == SDFR_F32 && store_dtype == SDFR_F32)
+            e = launch_fill_faces<float, float>(dsrc, g, st);
+        else if (src_dtype == SDFR_F32)
+            e = launch_fill_faces<float, __half>(dsrc, g, st);
+        else if (store_dtype == SDFR_F32)
+            e = launch_fill_faces<__half, float>(dsrc, g, st);
+        else
+            e = launch_fill_faces<__half, __half>(dsrc, g, st);
     }
     if (e == hipSuccess) e = hipStreamSynchronize(st);
     if (staged) (void)hipFree(staged);
@@ -1938,6 +2092,18 @@ SDFR_API int32_t sdfr_grid_set_march_events(SdfrGrid* grid, void* start, void* s
         return fail(-2, "sdfr_grid_set_march_events: give both events or neither");
     grid->march_events[0] = start;
     grid->march_events[1] = stop;
+    return 0;
+}
+
+SDFR_API int32_t sdfr_grid_set_border_faces(SdfrGrid* grid, int32_t mode) {
+    g_err[0] = '\0';
+    if (!grid) return fail(-1, "sdfr_grid_set_border_faces: null grid handle");
+    if (mode != SDFR_FACES_AUTO && mode != SDFR_FACES_ON && mode != SDFR_FACES_OFF)
+        return fail(-2, "sdfr_grid_set_border_faces: unknown mode %d", mode);
+    if (mode == SDFR_FACES_ON && !grid->has_faces)
+        return fail(-3, "sdfr_grid_set_border_faces: this grid keeps no face copies (they exist "
+                    "for f32 and f16 bricks)");
+    grid->border_faces = mode;
     return 0;
 }
 

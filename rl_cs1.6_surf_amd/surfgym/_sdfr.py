@@ -18,7 +18,7 @@ import torch  # noqa: F401  (load torch's HIP runtime first, see above)
 PKG_ROOT = Path(__file__).resolve().parents[1]
 LIB_PATH = PKG_ROOT / "lib" / "libsdfr.so"
 
-ABI_VERSION = 12
+ABI_VERSION = 13
 NOALLOC_SCRATCH_BYTES = 24 << 20   # SDFR_NOALLOC_SCRATCH_BYTES
 
 # element types (SDFR_* in sdfr.h)
@@ -27,10 +27,12 @@ LAYOUT_LINEAR, LAYOUT_BRICK4 = 0, 1
 CAM_EQUIANGULAR, CAM_PINHOLE = 0, 1
 SCHED_PERSISTENT, SCHED_TILES = 0, 1
 ORDER_LAUNCH, ORDER_LOOKAHEAD = 0, 1
+FACES_AUTO, FACES_ON, FACES_OFF = 0, 1, 2
 
 EXPORTS = ("sdfr_abi_version", "sdfr_last_error", "sdfr_grid_create", "sdfr_grid_destroy",
            "sdfr_grid_bytes", "sdfr_grid_attach_surfnz", "sdfr_grid_set_schedule",
-           "sdfr_grid_set_tile_order", "sdfr_grid_set_march_events", "sdfr_render_rays_per_lane",
+           "sdfr_grid_set_tile_order", "sdfr_grid_set_border_faces", "sdfr_grid_set_march_events",
+           "sdfr_render_rays_per_lane",
            "sdfr_workspace_bytes", "sdfr_render", "sdfr_render_noalloc", "sdfr_ray_dirs",
            "sdfr_grid_read",
            "sdfr_edt_workspace_bytes",
@@ -107,6 +109,8 @@ def load(path: Path | str | None = None):
     lib.sdfr_grid_set_schedule.argtypes = [vp, i32, i32, i32]
     lib.sdfr_grid_set_tile_order.restype = i32
     lib.sdfr_grid_set_tile_order.argtypes = [vp, i32, i64]
+    lib.sdfr_grid_set_border_faces.restype = i32
+    lib.sdfr_grid_set_border_faces.argtypes = [vp, i32]
     lib.sdfr_grid_set_march_events.restype = i32
     lib.sdfr_render_rays_per_lane.restype = i32
     lib.sdfr_render_rays_per_lane.argtypes = [vp, ctypes.POINTER(Cam), i32]

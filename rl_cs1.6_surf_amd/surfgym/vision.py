@@ -52,6 +52,7 @@ _OUT_DTYPES = {torch.float32: _sdfr.F32, torch.bfloat16: _sdfr.BF16}
 _LAYOUTS = {"linear": _sdfr.LAYOUT_LINEAR, "brick4": _sdfr.LAYOUT_BRICK4}
 _SCHEDULES = {"persistent": _sdfr.SCHED_PERSISTENT, "tiles": _sdfr.SCHED_TILES}
 _TILE_ORDERS = {"launch": _sdfr.ORDER_LAUNCH, "lookahead": _sdfr.ORDER_LOOKAHEAD}
+_BORDER_FACES = {"auto": _sdfr.FACES_AUTO, "on": _sdfr.FACES_ON, "off": _sdfr.FACES_OFF}
 
 
 def pick_cell(core, budget_voxels: float = 700e6) -> float:
@@ -407,6 +408,7 @@ class GpuLidar:
             _sdfr.check(rc, "sdfr_grid_attach_surfnz", self._lib)
         self.set_schedule(schedule, refill_lanes, rays_per_lane)
         self.set_tile_order(tile_order)
+        self.border_faces = "auto"   # see set_border_faces
 
     def set_schedule(self, schedule: str = "tiles", refill_lanes: int = 16,
                      rays_per_lane: int | None = None) -> None:
@@ -448,6 +450,19 @@ class GpuLidar:
         _sdfr.check(self._lib.sdfr_grid_set_tile_order(self._grid, _TILE_ORDERS[order], mt),
                     "sdfr_grid_set_tile_order", self._lib)
         self.tile_order = order
+
+    def set_border_faces(self, mode: str = "auto") -> None:
+        """When the one-ray-per-lane march reads border voxels (every
+        sample outside the grid clamps to one, vision.py:104-106) from the
+        grid's 2D face copies instead of its bricks: "auto" (the default: on
+        grids beyond the Infinity Cache, above 192 MiB), "on" or "off". The
+        copies exist for fp32 and fp16 bricks; they hold the bricks'
+        values, so results are unchanged."""
+        if mode not in _BORDER_FACES:
+            raise ValueError(f"border faces must be one of {sorted(_BORDER_FACES)}, got {mode!r}")
+        _sdfr.check(self._lib.sdfr_grid_set_border_faces(self._grid, _BORDER_FACES[mode]),
+                    "sdfr_grid_set_border_faces", self._lib)
+        self.border_faces = mode
 
     def set_march_events(self, start: int | None, stop: int | None) -> None:
         """Measurement hook: raw hipEvent_t handles (ints) that every later

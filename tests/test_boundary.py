@@ -116,6 +116,16 @@ def test_schedule_and_tile_order_reject_a_null_handle_without_a_device():
     assert "null grid" in _sdfr.last_error()
     assert lib.sdfr_grid_set_march_events(None, None, None) == -1
     assert "null grid" in _sdfr.last_error()
+    assert lib.sdfr_grid_set_border_faces(None, _sdfr.FACES_ON) == -1
+    assert "null grid" in _sdfr.last_error()
+
+
+def test_border_face_modes_match_the_header():
+    from surfgym import _sdfr
+    text = (ROOT / "include" / "sdfr.h").read_text()
+    for name, value in (("AUTO", _sdfr.FACES_AUTO), ("ON", _sdfr.FACES_ON),
+                        ("OFF", _sdfr.FACES_OFF)):
+        assert re.search(rf"SDFR_FACES_{name} = {value}\b", text), name
 
 
 def test_render_rejects_bad_arguments_without_a_device():

@@ -2,7 +2,8 @@
 (one voxel thick along any axis, a single voxel, partial bricks) in every
 store and layout, eyes outside the grid on every side (every sample then
 reads the clamped border voxel first, vision.py:644-646), and grids whose
-cell or origin keeps the voxel index in subtract-then-scale form."""
+cell or origin keeps the voxel index in subtract-then-scale form; where the
+grid keeps border face copies, with the march reading them and not."""
 from __future__ import annotations
 
 import numpy as np
@@ -29,6 +30,10 @@ def _field(shape, seed):
     for z, y, x in pts:
         d = np.minimum(d, np.sqrt((zz - z) ** 2 + (yy - y) ** 2 + (xx - x) ** 2))
     return (d * 16.0).astype(np.float32)
+
+
+def _has_faces(store, layout):
+    return store in ("f32", "f16") and layout == "brick4"
 
 
 def _poses(shape, n, seed, outside=False):
@@ -58,11 +63,14 @@ def test_degenerate_grid_shapes(dev, shape, gdt, store, layout):
     kw = dict(width=24, height=10, range_units=900.0, near_range=400.0, max_steps=48)
     lid = vision.GpuLidar.from_grid(g, np.zeros(3), 16.0, grid_dtype=gdt, layout=layout,
                                     device=dev, **kw)
-    for order in ("lookahead", "launch"):
-        lid.set_tile_order(order, min_tiles=0)
-        got = lid.render(*[torch.as_tensor(a, device=dev) for a in (o, yaw, pitch, duck)])
-        want, _ = oracle.render(g, np.zeros(3), 16.0, o, yaw, pitch, duck, store=store, **kw)
-        assert np.array_equal(got.cpu().numpy(), want), order
+    want, _ = oracle.render(g, np.zeros(3), 16.0, o, yaw, pitch, duck, store=store, **kw)
+    faces = ("off", "on") if _has_faces(store, layout) else ("auto",)
+    for mode in faces:
+        lid.set_border_faces(mode)
+        for order in ("lookahead", "launch"):
+            lid.set_tile_order(order, min_tiles=0)
+            got = lid.render(*[torch.as_tensor(a, device=dev) for a in (o, yaw, pitch, duck)])
+            assert np.array_equal(got.cpu().numpy(), want), (mode, order)
 
 
 @pytest.mark.parametrize("gdt,store,layout", _STORES)
@@ -75,9 +83,28 @@ def test_eyes_outside_the_grid(dev, gdt, store, layout):
     kw = dict(width=32, height=16, range_units=1500.0, near_range=600.0, max_steps=64)
     lid = vision.GpuLidar.from_grid(g, np.full(3, -8.0), 16.0, grid_dtype=gdt, layout=layout,
                                     device=dev, **kw)
-    got = lid.render(*[torch.as_tensor(a, device=dev) for a in (o, yaw, pitch, duck)])
     want, _ = oracle.render(g, np.full(3, -8.0), 16.0, o, yaw, pitch, duck, store=store, **kw)
-    assert np.array_equal(got.cpu().numpy(), want)
+    for mode in (("off", "on") if _has_faces(store, layout) else ("auto",)):
+        lid.set_border_faces(mode)
+        for rpl in (1, 2):
+            lid.set_schedule("tiles", rays_per_lane=rpl)
+            got = lid.render(*[torch.as_tensor(a, device=dev) for a in (o, yaw, pitch, duck)])
+            assert np.array_equal(got.cpu().numpy(), want), (mode, rpl)
+
+
+def test_border_faces_exist_for_f32_and_f16_bricks(dev):
+    """set_border_faces("on") is refused where the grid keeps no face
+    copies (r16 bricks, the linear layout); "auto" and "off" are accepted."""
+    g = _field((6, 7, 9), 2)
+    for gdt, layout in (("r16", "brick4"), (torch.float32, "linear"), (torch.float16, "linear")):
+        lid = vision.GpuLidar.from_grid(g, np.zeros(3), 16.0, grid_dtype=gdt, layout=layout,
+                                        device=dev, width=8, height=8)
+        lid.set_border_faces("auto")
+        lid.set_border_faces("off")
+        with pytest.raises(Exception, match="face copies"):
+            lid.set_border_faces("on")
+    with pytest.raises(ValueError):
+        lid.set_border_faces("always")
 
 
 @pytest.mark.parametrize("cell,mins", [(12.0, (-8.0, -8.0, -8.0)), (24.0, (3.0, -5.0, 0.0)),
@@ -99,6 +126,8 @@ def test_grids_without_the_single_rounding_index(dev, cell, mins, gdt, store, la
     want, _ = oracle.render(g, mins, cell, o, yaw, pitch, duck, store=store, **kw)
     lid = vision.GpuLidar.from_grid(g, mins, cell, grid_dtype=gdt, layout=layout, device=dev, **kw)
     args = [torch.as_tensor(a, device=dev) for a in (o, yaw, pitch, duck)]
+    if _has_faces(store, layout):
+        lid.set_border_faces("on")
     for rpl in (1, 2):
         lid.set_schedule("tiles", rays_per_lane=rpl)
         for order in ("launch", "lookahead"):

@@ -5,7 +5,7 @@ camera (size, field of view, equiangular or pinhole, optionally the
 surf-mask channel), the step rule (range, near, hit_eps, min_step,
 max_steps), a batch of poses inside and outside the grid, and a library
 configuration (store, layout, schedule, rays per lane, tile order, output
-dtype, census). The image must equal the oracle's on the grid as stored bit
+dtype, census, border faces). The image must equal the oracle's on the grid as stored bit
 for bit (bf16: the oracle's fp32 encodings rounded to nearest even), and the
 census its per-ray load counts. The sweep reaches combinations the fixed
 tests do not: odd image sizes against the 16x4 tiles, step budgets from 0 to
@@ -67,7 +67,9 @@ def _case(seed):
     lib = dict(schedule=str(rng.choice(["tiles", "tiles", "persistent"])),
                rays_per_lane=[None, 1, 2][int(rng.integers(0, 3))],
                order=str(rng.choice(["launch", "lookahead"])),
-               out=str(rng.choice(["f32", "bf16"])), census=bool(rng.random() < 0.5))
+               out=str(rng.choice(["f32", "bf16"])), census=bool(rng.random() < 0.5),
+               faces=str(rng.choice(["auto", "on", "off"])) if store != "r16" and layout == "brick4"
+               else "auto")
     snz = rng.integers(0, 128, shape).astype(np.int8) if surf else None
     return grid, mins, cell, poses, cam, store, layout, lib, snz
 
@@ -85,6 +87,7 @@ def test_random_render_equals_the_oracle(dev, seed):
                                     device=dev, **cam)
     lid.set_schedule(lib["schedule"], rays_per_lane=lib["rays_per_lane"])
     lid.set_tile_order(lib["order"], min_tiles=0)
+    lid.set_border_faces(lib["faces"])
     ch = (2,) if snz is not None else ()
     odt = torch.bfloat16 if lib["out"] == "bf16" else torch.float32
     out = torch.full((n, cam["height"], cam["width"]) + ch, -1.0, dtype=odt, device=dev)
