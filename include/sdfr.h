@@ -82,7 +82,8 @@ enum {
 /* When the one-ray march reads border voxels from the grid's face copies
  * (f32/f16 bricks keep each of the six border layers again as a 2D copy). */
 enum {
-    SDFR_FACES_AUTO = 0,  /* default: for grids beyond the Infinity Cache (above 192 MiB) */
+    SDFR_FACES_AUTO = 0,  /* default: for grids beyond the Infinity Cache (above 192 MiB) in
+                             renders of at least 16384 tiles (128 envs of 128x64) */
     SDFR_FACES_ON = 1,    /* whenever the march runs one ray per lane */
     SDFR_FACES_OFF = 2    /* never */
 };

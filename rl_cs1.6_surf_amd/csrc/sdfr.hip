@@ -149,6 +149,9 @@ constexpr int64_t kSmallRenderTiles = 1 << 16;
 #define SDFR_INLINE_SETUP_TILES (1 << 13)
 #endif
 constexpr int64_t kInlineSetupTiles = SDFR_INLINE_SETUP_TILES;
+// Renders of at least this many tiles (128 envs of 128x64) read border
+// voxels from the face copies on grids beyond the Infinity Cache.
+constexpr int64_t kFacesMinTiles = 1 << 14;
 
 // ---------------------------------------------------------------- errors --
 thread_local char g_err[512];
@@ -1628,9 +1631,16 @@ int32_t render_impl(const char* fn, const SdfrGrid* grid, const SdfrCam* cam, co
     a.order_units = (a.total_tiles + a.order_unit - 1) / a.order_unit;
     a.logical_tiles = a.total_tiles;
     a.inline_setup = 0;
+    // border face copies: by default for grids beyond the Infinity Cache in
+    // renders of at least kFacesMinTiles tiles (the lookup lengthens every
+    // step's chain of dependent instructions, which is what a small render's
+    // time is made of: winding_track at 1 / 16 / 64 envs 26.4 / 53.6 / 123
+    // us without, 35.1 / 62.2 / 127 with; at 256 / 512 envs 342 / 594 without,
+    // 315 / 528 with)
     a.faces = grid->has_faces &&
               (grid->border_faces == SDFR_FACES_ON ||
-               (grid->border_faces == SDFR_FACES_AUTO && grid->store_bytes > kCacheResidentBytes));
+               (grid->border_faces == SDFR_FACES_AUTO && grid->store_bytes > kCacheResidentBytes &&
+                a.total_tiles >= kFacesMinTiles));
     a.face_alog = grid->store_dtype == SDFR_F32 ? 3 : 4;
     a.face_lines_x = grid->face_lines[0];
     a.face_lines_y = grid->face_lines[1];

@@ -455,7 +455,9 @@ class GpuLidar:
         """When the one-ray-per-lane march reads border voxels (every
         sample outside the grid clamps to one, vision.py:104-106) from the
         grid's 2D face copies instead of its bricks: "auto" (the default: on
-        grids beyond the Infinity Cache, above 192 MiB), "on" or "off". The
+        grids beyond the Infinity Cache, above 192 MiB, in renders of at
+        least 128 envs of 128x64; smaller renders are latency-bound and the
+        lookup lengthens every step), "on" or "off". The
         copies exist for fp32 and fp16 bricks; they hold the bricks'
         values, so results are unchanged."""
         if mode not in _BORDER_FACES:
