@@ -99,10 +99,12 @@ static_assert(kOrderBuckets % 256 == 0, "the sort blocks' 256 threads take 16 bu
 // Lookahead distance of the tile order, in units of the near range: where a
 // unit's centre ray is this far out keys the unit. Grids beyond the Infinity
 // Cache key further out (their rays' working sets are what the order has to
-// keep apart): on the 1 GiB track 1.5 beat 1.2 by 1.5% and 2.0 by 0.4%;
-// on the cache-resident grids 1.2 is within noise of the best (1.0-1.2).
+// keep apart): on the 1 GiB track, with its border voxels read from the
+// face copies, 3.0 beats 1.5 by 0.9-2.7% at 1024-4096 envs (2.0: 2.6%
+// slower); on the cache-resident grids 1.2 is within noise of the best
+// (1.0-1.2).
 constexpr float kOrderLookahead = 1.2f;
-constexpr float kOrderLookaheadSpilled = 1.5f;
+constexpr float kOrderLookaheadSpilled = 3.0f;
 // Renders of fewer tiles skip the sort by default: its two launches cost
 // ~9 us, more than it saves below ~512 envs of 128x64.
 constexpr int64_t kOrderMinTiles = 1 << 16;
