@@ -90,7 +90,10 @@ constexpr int64_t kCacheResidentBytes = 192ll << 20;
 // tiles schedule then holds at most this many workgroups per CU (by sizing
 // their LDS), 24 waves instead of 32. Measured on a 1 GiB grid: 12 per CU
 // 2.09 ms, 10 2.10, 16 (unlimited) 2.15, 5 2.55; on a cache-resident grid any
-// cap is slower.
+// cap is slower. A march that reads border voxels from the face copies
+// misses less and is faster uncapped (1 GiB f32 grid, 2048 envs: 1.842 ms
+// capped at 12, 1.811 uncapped; 512 MiB f16 1.665 / 1.626), so the cap holds
+// only without them (f32 2.026 / 2.037, r16 2.704 / 2.834).
 constexpr int kSpillBlocksPerCU = 12;
 // Tile order: 16 cells per axis at most, Morton-numbered buckets.
 constexpr int kOrderCellsLog = 4;
@@ -1395,7 +1398,7 @@ struct MarchPlan {
 template <typename GT, int LAYOUT, int OUT, int CAMERA, bool CENSUS, bool SURF>
 MarchPlan plan_tiles(MarchArgs& a, const SdfrGrid* g) {
     size_t lds = axis_lds_bytes(a);
-    if (g->store_bytes > kCacheResidentBytes && g->lds_per_cu > 0)
+    if (g->store_bytes > kCacheResidentBytes && !a.faces && g->lds_per_cu > 0)
         lds = max(lds, (size_t)g->lds_per_cu / kSpillBlocksPerCU);   // cap the workgroups per CU
     const int per_block = kTileWaves * a.rpl;
     const int64_t blocks = (a.logical_tiles + per_block - 1) / per_block;
@@ -1639,7 +1642,9 @@ int32_t render_impl(const char* fn, const SdfrGrid* grid, const SdfrCam* cam, co
     // time is made of: winding_track at 1 / 16 / 64 envs 26.4 / 53.6 / 123
     // us without, 35.1 / 62.2 / 127 with; at 256 / 512 envs 342 / 594 without,
     // 315 / 528 with)
-    a.faces = grid->has_faces &&
+    // (only the one-ray march reads them, so the flag says whether this
+    // render's march does)
+    a.faces = grid->has_faces && a.rpl == 1 &&
               (grid->border_faces == SDFR_FACES_ON ||
                (grid->border_faces == SDFR_FACES_AUTO && grid->store_bytes > kCacheResidentBytes &&
                 a.total_tiles >= kFacesMinTiles));
