@@ -22,7 +22,7 @@ from surfgym import vision
 
 pytestmark = pytest.mark.gpu
 
-N_CASES = 160
+N_CASES = 600
 
 
 def _field(rng, shape, cell):
