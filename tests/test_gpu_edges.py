@@ -138,6 +138,36 @@ def test_grids_without_the_single_rounding_index(dev, cell, mins, gdt, store, la
             assert np.array_equal(got.cpu().numpy(), want), (cell, rpl, order)
 
 
+@pytest.mark.parametrize("eps", [16.0, 16.003, 0.0, -3.0, 70000.0, 1e-6, float("inf")])
+def test_fp16_samples_against_hit_eps_at_every_rounding(dev, eps):
+    """fp16 bricks compare each sample with hit_eps without converting it
+    (against the largest fp16 value <= hit_eps). Grid values at and a few
+    fp16 steps either side of hit_eps (and of its fp16 floor), with hit_eps
+    exact in fp16, between two fp16 values, zero, negative, beyond the fp16
+    range and infinite: every image equals the oracle's on the f16-rounded
+    grid, one and two rays per lane."""
+    rng = np.random.default_rng(17)
+    shape = (6, 7, 8)
+    e16 = np.float16(np.clip(eps, -65504.0, 65504.0)) if np.isfinite(eps) else np.float16(60000.0)
+    steps = np.arange(-3, 4)
+    bits = (e16.view(np.uint16).astype(np.int32) + np.where(e16 < 0, -steps, steps)).astype(np.uint16)
+    near = bits.view(np.float16).astype(np.float32)
+    near = near[np.isfinite(near)]
+    g = rng.choice(np.concatenate([near, np.float32([0.0, 40.0, 300.0])]), size=shape).astype(np.float32)
+    n = 6
+    o, yaw, pitch, duck = _poses(shape, n, 19)
+    kw = dict(width=24, height=8, range_units=700.0, near_range=300.0, max_steps=24, hit_eps=eps,
+              min_step=4.0)
+    want, _ = oracle.render(g, np.zeros(3), 16.0, o, yaw, pitch, duck, store="f16", **kw)
+    lid = vision.GpuLidar.from_grid(g, np.zeros(3), 16.0, grid_dtype=torch.float16, device=dev, **kw)
+    args = [torch.as_tensor(a, device=dev) for a in (o, yaw, pitch, duck)]
+    for rpl in (1, 2):
+        lid.set_schedule("tiles", rays_per_lane=rpl)
+        print(f"case edges fp16 hit_eps={eps} rpl={rpl}", flush=True)
+        got = lid.render(*args)
+        assert np.array_equal(got.cpu().numpy(), want), (eps, rpl)
+
+
 def test_the_largest_batch_renders_every_env(dev):
     """The largest batch the library accepts at 128x64 (2^31 - 1 rays):
     262,140 envs, four distinct poses repeated, so the image offsets reach
