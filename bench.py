@@ -41,10 +41,17 @@ def _log(msg):
     print(msg, file=sys.stderr, flush=True)
 
 
-def cpu_baseline(w, sc, envs, repeats=5):
-    """Lockstep torch render (the reference's CPU path shape) on host cores."""
+def cpu_baseline(w, sc, envs, repeats=5, image=None):
+    """Lockstep torch render (the reference's CPU path shape) on host cores.
+
+    With ``image`` (the GPU render of the same ``envs`` poses, (N,H,W) f32)
+    it also reports ``agreement``: one more lockstep render, untimed, that
+    keeps its per-ray depths and directions, compared ray by ray with the
+    GPU image at the north star's tolerance (0.5 u in depth, 1e-3 in the
+    encoding), every ray outside it re-traced and classified
+    (oracle/agreement.py)."""
     import torch
-    from oracle import lockstep
+    from oracle import agreement, lockstep
     cores = len(os.sched_getaffinity(0))
     torch.set_num_threads(cores)
     ps = w.poses(sc, envs)
@@ -56,6 +63,25 @@ def cpu_baseline(w, sc, envs, repeats=5):
         lockstep.render(sc.sdf, sc.mins, sc.cell, ps.origin, ps.yaw, ps.pitch, ps.ducked, **kw)
         times.append(time.perf_counter() - t0)
     t = statistics.median(times)
+    agree = None
+    if image is not None:
+        keep = {}
+        ref = lockstep.render(sc.sdf, sc.mins, sc.cell, ps.origin, ps.yaw, ps.pitch, ps.ducked,
+                              keep=keep, **kw)
+        agree = agreement.compare(sc.sdf, sc.mins, sc.cell, ps.origin, ps.yaw, ps.pitch,
+                                  ps.ducked, image, ref, keep, list_max=None, **kw)
+        del keep, ref
+        listed = agree.pop("listed")
+        steps = [o for o in listed if o["class"] == "step_phase"]
+        agree["step_phase_max_depth_over_last_step"] = (
+            round(max(abs(o["depth"] - o["depth_ref"]) / o["last_step_u"] for o in steps), 4)
+            if steps else None)
+        agree["not_step_phase"] = [o for o in listed if o["class"] != "step_phase"][:16]
+        _log(f"[bench] agreement with the torch lockstep: {agree['exact']:.5%} bit-identical, "
+             f"{agree['within_tol']:.5%} within tolerance, {agree['outliers']} outliers "
+             f"({agree['outliers_grazing']} grazing, {agree['outliers_step_phase']} one step "
+             f"apart, {agree['outliers_tie_other']} other after a face tie, "
+             f"{agree['outliers_other']} unexplained)")
     rays = envs * w.width * w.height
     model = ""
     try:
@@ -68,7 +94,8 @@ def cpu_baseline(w, sc, envs, repeats=5):
     return {"value": round(rays / t / 1e9, 6), "unit": "G rays/s", "cores": cores,
             "kind": "port",
             "sample": f"{envs} of {w.n_envs} envs of {w.name} ({rays} rays), torch lockstep, "
-                      f"median of {repeats}: {t * 1e3:.1f} ms; cpu: {model}"}
+                      f"median of {repeats}: {t * 1e3:.1f} ms; cpu: {model}",
+            "agreement": agree}
 
 
 class HipEvents:
@@ -507,8 +534,87 @@ def measure_render(w, args, dev, *, graph, steps, warmup, out_shape=None, sc=Non
            "out": w.out_dtype, "out_shape": list(out.shape), "graph": bool(graph),
            "ms_per_step": ms_per_step, "launch_ms_median": statistics.median(launch_ms),
            "march_kernel_ms_avg": kernel_ms, "loads": loads, "alg_bytes": alg_bytes,
-           "census": census, "rpl": lid.effective_rays_per_lane(n)}
+           "census": census, "rpl": lid.effective_rays_per_lane(n), "image": out}
     return res
+
+
+# The reference's lidar phase per 128-decision PPO iteration after its early-exit
+# kernel (docs/perf-results.md:86, :415): RTX 5090, surf_src_cannonball (fp16
+# grid at 32 u), the live fleet's poses. Context, not a same-scene figure.
+REFERENCE_LIDAR_PHASE_MS = 190.4
+
+
+def lidar_phase(w, args, dev, sc, decisions=128):
+    """The trainer's per-decision lidar work for one PPO iteration of
+    `decisions` decisions (train_fast.py:1744-1765, the `lidar` phase of
+    docs/perf-results.md): each decision copies the (N, 6) pinned pose block
+    to the device, then renders from its column views, either straight into
+    the image columns of the (N, 15 + H*W) observation row (`out=`) or, as
+    the reference does, into a new tensor that is then copied into those
+    columns. HIP events bracket each decision's render (+ copy), as the
+    trainer's phase timer does, and the whole iteration (+ pose copies)."""
+    import torch
+    from surfgym import vision
+    ps = w.poses(sc)
+    n = len(ps)
+    gdt = {"f32": torch.float32, "f16": torch.float16, "r16": "r16"}[w.store]
+    lid = vision.GpuLidar.from_grid(sc.sdf, sc.mins, sc.cell, width=w.width, height=w.height,
+                                    range_units=w.range_units, near_range=w.near_range,
+                                    max_steps=w.max_steps, hit_eps=w.hit_eps, grid_dtype=gdt,
+                                    layout=args.layout, schedule=args.schedule,
+                                    refill_lanes=args.refill, rays_per_lane=args.rpl,
+                                    tile_order=args.tile_order, device=dev)
+    pin = torch.empty(n, 6, dtype=torch.float32, pin_memory=True)
+    pin[:, 0:3] = torch.as_tensor(ps.origin)
+    pin[:, 3] = torch.as_tensor(ps.yaw)
+    pin[:, 4] = torch.as_tensor(ps.pitch)
+    pin[:, 5] = torch.as_tensor(np.asarray(ps.ducked, np.float32))
+    vis = torch.empty(n, 6, device=dev)
+    scalars = 15
+    obs = torch.zeros(n, scalars + w.width * w.height, device=dev)
+
+    def fused():
+        lid.render(vis[:, 0:3], vis[:, 3], vis[:, 4], vis[:, 5], out=obs[:, scalars:])
+
+    def reference():
+        img = lid.render(vis[:, 0:3], vis[:, 3], vis[:, 4], vis[:, 5])
+        obs[:, scalars:].copy_(img.reshape(n, -1))
+
+    stream = torch.cuda.current_stream(dev)
+    sp = stream.cuda_stream
+    out = {"workload": w.name, "envs": n, "decisions": decisions,
+           "obs_row": f"({n}, {scalars}+{w.height}*{w.width}) f32"}
+    images = {}
+    for name, body in (("fused", fused), ("reference_sequence", reference)):
+        obs.zero_()
+        for _ in range(5):
+            vis.copy_(pin, non_blocking=True)
+            body()
+        ev = HipEvents(2 + 2 * decisions)
+        torch.cuda.synchronize()
+        ev.record(0, sp)
+        for k in range(decisions):
+            vis.copy_(pin, non_blocking=True)
+            ev.record(2 + 2 * k, sp)
+            body()
+            ev.record(3 + 2 * k, sp)
+        ev.record(1, sp)
+        torch.cuda.synchronize()
+        phase = sum(ev.ms(2 + 2 * k, 3 + 2 * k) for k in range(decisions))
+        out[f"{name}_phase_ms"] = round(phase, 3)
+        out[f"{name}_iteration_ms"] = round(ev.ms(0, 1), 3)
+        ev.close()
+        images[name] = obs[:, scalars:].clone()
+    out["identical"] = bool(torch.equal(images["fused"], images["reference_sequence"]))
+    out["phase_saved_ms"] = round(out["reference_sequence_phase_ms"] - out["fused_phase_ms"], 3)
+    out["reference_published_phase_ms"] = REFERENCE_LIDAR_PHASE_MS
+    out["reference_published_context"] = ("RTX 5090, surf_src_cannonball fp16 grid at 32 u, the "
+                                          "live fleet's poses (docs/perf-results.md:86, :415)")
+    _log(f"[bench] lidar phase, {decisions} decisions of {n} envs: fused "
+         f"{out['fused_phase_ms']:.2f} ms, render + copy {out['reference_sequence_phase_ms']:.2f} "
+         f"ms (the reference's: {REFERENCE_LIDAR_PHASE_MS} ms on its scene and card)")
+    del lid
+    return out
 
 
 def config_summary(r, traffic=None, traffic_src=None, limiter=None):
@@ -546,6 +652,7 @@ def bench_steps_sweep(args, w, dev, shape):
                            steps=args.steps, warmup=args.warmup, out_shape=shape, sc=sc)
         r.pop("lid")
         r.pop("sc")
+        r.pop("image")
         rows.append({"max_steps": cap, "ms_per_batch": round(r["ms_per_step"], 5),
                      "march_kernel_ms_avg": round(r["march_kernel_ms_avg"], 5),
                      "g_rays_per_s": round(r["rays"] / (r["ms_per_step"] * 1e-3) / 1e9, 4),
@@ -618,7 +725,11 @@ def main(argv=None):
         return bench_steps_sweep(args, w, dev, shape)
     r = measure_render(w, args, dev, graph=args.graph, steps=args.steps, warmup=args.warmup,
                        out_shape=shape)
-    sc, lid = r.pop("sc"), r.pop("lid")
+    sc, lid, image = r.pop("sc"), r.pop("lid"), r.pop("image")
+    # the last timed render's image, kept for the agreement with the CPU render
+    image = (image.float().cpu().numpy()
+             if not args.no_cpu and tuple(image.shape) == (r["envs"], w.height, w.width)
+             else None)
     n, rays = r["envs"], r["rays"]
     ms_per_step, kernel_ms = r["ms_per_step"], r["march_kernel_ms_avg"]
     achieved = r["alg_bytes"] / (kernel_ms * 1e-3) / 1e9
@@ -644,7 +755,11 @@ def main(argv=None):
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
+        # the march's arithmetic is fp32 whatever the store: fp16 and r16
+        # voxels are widened to fp32 as they are read
         "dtype": "f32",
+        "grid_dtype": w.store,
+        "out_dtype": w.out_dtype,
         "data": "synthetic",
         "config": {"workload": w.name, "envs": n, "image": f"{w.width}x{w.height}",
                    "rays": rays, "grid": r["grid"],
@@ -680,16 +795,20 @@ def main(argv=None):
                                 warmup=min(args.warmup, 5), out_shape=shape)
             order = cr.pop("lid").tile_order
             cr.pop("sc")
+            cr.pop("image")
             ct, ct_src = profiled(f"{name} {args.schedule} rpl={cr['rpl']} {args.layout} {cw.store}"
                                   f" order={order}", traffic_tab, "bytes")
             cl, _ = profiled(name, limiter_tab)
             configs[name] = config_summary(cr, ct, ct_src, cl)
             torch.cuda.empty_cache()
+        configs["lidar_phase"] = lidar_phase(w, args, dev, sc)
+        torch.cuda.empty_cache()
         res["configs"] = configs
     if not args.no_cpu:
         envs = min(args.cpu_envs, n)
         _log(f"[bench] cpu baseline on {envs} envs ...")
-        res["cpu_baseline"] = cpu_baseline(w, sc, envs)
+        res["cpu_baseline"] = cpu_baseline(w, sc, envs,
+                                           image=image if envs == n else None)
     print(json.dumps(res), flush=True)
 
 

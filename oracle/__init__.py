@@ -12,6 +12,9 @@ its goal field:
   tools/bench_lidar.py:45-88), which is the algorithmic-bytes count.
 * :mod:`oracle.goal` — the goal-field bake and sampler
   (python/surfgym/goalfield.py), ``oracle/goal.c``.
+* :mod:`oracle.agreement` — a render compared with the lockstep render
+  (the reference's CPU arithmetic) at the north star's tolerance, every
+  ray outside it re-traced and classified.
 * :mod:`oracle.lockstep` — the reference's CPU fallback shape
   (``_render_torch``, vision.py:626-666): torch tensors over all rays in
   lockstep, with a host ``any()`` check every 8 steps. It is the CPU
@@ -78,6 +81,9 @@ def _load():
     lib.oracle_encode.argtypes = [f, f]
     lib.oracle_march_ray.restype = f
     lib.oracle_march_ray.argtypes = [p, i, i, i, p, f, f, f, f, f, f, f, f, f, f, i, p]
+    lib.oracle_march_trace.restype = i
+    lib.oracle_march_trace.argtypes = [p, i, i, i, p, f, f, f, f, f, f, f, f, f, f, i, i,
+                                       p, p, p, p, p, p]
     lib.oracle_render.restype = i
     lib.oracle_render.argtypes = [p, i, i, i, p, f, i, i, i, d, d, d, d, f, f, f, f, i,
                                   p, p, p, p, i, p, p, p, i]

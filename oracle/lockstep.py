@@ -30,8 +30,13 @@ def _equiangular_tables(width, height, hfov_deg, vfov_deg):
 @torch.no_grad()
 def render(grid, mins, cell, origin, yaw_deg, pitch_deg, ducked, *, width=128, height=64,
            hfov_deg=120.0, vfov_deg=90.0, range_units=2000.0, near_range=None, hit_eps=None,
-           min_step=None, max_steps=64, env_chunk=64):
-    """(N,H,W) f32 encodings, computed on the CPU with torch in lockstep."""
+           min_step=None, max_steps=64, env_chunk=64, keep=None):
+    """(N,H,W) f32 encodings, computed on the CPU with torch in lockstep.
+
+    ``keep``: a dict that receives the march's own per-ray values, ``t``
+    (N,H,W) f32 depths (clamped to the range) and ``dirs`` (N,H,W,3) f32
+    directions as torch computed them, so a comparison can re-trace any ray
+    exactly as this render marched it."""
     g = torch.as_tensor(np.ascontiguousarray(grid, np.float32)).reshape(-1)
     nz, ny, nx = np.shape(grid)
     mins_t = torch.as_tensor(np.asarray(mins, np.float32).reshape(3))
@@ -48,6 +53,9 @@ def render(grid, mins, cell, origin, yaw_deg, pitch_deg, ducked, *, width=128, h
     yoff, poff = _equiangular_tables(width, height, hfov_deg, vfov_deg)
     n_all = origin.shape[0]
     out = torch.empty(n_all, height, width)
+    if keep is not None:
+        keep["t"] = np.empty((n_all, height, width), np.float32)
+        keep["dirs"] = np.empty((n_all, height, width, 3), np.float32)
     for a in range(0, n_all, env_chunk):
         b = min(n_all, a + env_chunk)
         n = b - a
@@ -75,6 +83,9 @@ def render(grid, mins, cell, origin, yaw_deg, pitch_deg, ducked, *, width=128, h
             if (k & 7) == 7 and not bool(alive.any()):
                 break
         t = torch.clamp(t, max=rng)
+        if keep is not None:
+            keep["t"][a:b] = t.view(n, height, width).numpy()
+            keep["dirs"][a:b] = torch.stack((dx, dy, dz), 1).view(n, height, width, 3).numpy()
         enc = (torch.clamp(t, max=near) / near
                + 0.25 * (1.0 - torch.exp(-torch.clamp(t - near, min=0.0) / 2500.0)))
         out[a:b] = enc.view(n, height, width)

@@ -145,6 +145,42 @@ ORACLE_API float oracle_march_ray(const float* grid, int nx, int ny, int nz, con
     return t;
 }
 
+/* oracle_march_ray with a record of every sample it takes: for step k,
+ * t_k[k] (the distance the sample is taken at), vox[3k..3k+2] (ix, iy, iz),
+ * pos[3k..3k+2] (the unclamped voxel coordinates ((e + d*t) - mins) * inv_cell,
+ * whose distance to the nearest integer is the sample's distance to a voxel
+ * face in cells) and s_k[k] (the value read). Stores at most cap records;
+ * returns the number of samples taken and writes the final t and the stop
+ * reason (0 hit: s <= hit_eps, 1 range: t >= range, 2 steps exhausted). */
+ORACLE_API int oracle_march_trace(const float* grid, int nx, int ny, int nz, const float* mins,
+                                  float inv_cell, float ex, float ey, float ez, float dx, float dy,
+                                  float dz, float range, float hit_eps, float min_step,
+                                  int max_steps, int cap, float* t_k, int32_t* vox, float* pos,
+                                  float* s_k, float* t_final, int32_t* why) {
+    float t = 0.0f;
+    int k = 0, reason = 2;
+    for (; k < max_steps; ++k) {
+        const float fx = ((ex + dx * t) - mins[0]) * inv_cell;
+        const float fy = ((ey + dy * t) - mins[1]) * inv_cell;
+        const float fz = ((ez + dz * t) - mins[2]) * inv_cell;
+        const int ix = clamp_index(fx, nx), iy = clamp_index(fy, ny), iz = clamp_index(fz, nz);
+        const float s = grid[((size_t)iz * (size_t)ny + (size_t)iy) * (size_t)nx + (size_t)ix];
+        if (k < cap) {
+            t_k[k] = t;
+            vox[3 * k] = ix; vox[3 * k + 1] = iy; vox[3 * k + 2] = iz;
+            pos[3 * k] = fx; pos[3 * k + 1] = fy; pos[3 * k + 2] = fz;
+            s_k[k] = s;
+        }
+        if (!(s > hit_eps)) { reason = 0; ++k; break; }
+        if (!(t < range)) { reason = 1; ++k; break; }
+        const float st = s * 0.9f;
+        t = t + (st > min_step ? st : min_step);
+    }
+    *t_final = t;
+    *why = reason;
+    return k;
+}
+
 /* Full render of N envs into out[N][H][W] (and loads[N][H][W] if given).
  * grid holds the voxel values exactly as the renderer reads them (an f16
  * store is emulated by the caller rounding to f16 and back). Poses are

@@ -1,0 +1,55 @@
+"""GPU render against the reference's own CPU arithmetic at the headline size.
+
+The reference's CPU render (python/surfgym/vision.py:596-657) takes cos/sin/
+exp from torch's CPU kernels; oracle/lockstep.py restates it with those same
+calls. This renders all 2048 ramp_field envs (16.8 M rays) on the GPU, the
+same poses through the lockstep on this host's cores, and holds the pair to
+the north star's bar: >= 99.9% of rays within 0.5 u of the reference's depth
+and 1e-3 of its encoding, every ray outside it classified by
+oracle/agreement.py, and every outlier's GPU value reproduced by the
+oracle's march. None may be unexplained (class "other": two marches that part
+away from a voxel face); this host's torch build decides how many last-bit
+differences there are, so the other classes are counted, not fixed.
+"""
+from __future__ import annotations
+
+import os
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import agreement, lockstep
+from surfgym import synth, vision
+
+pytestmark = pytest.mark.gpu
+
+
+def test_headline_render_meets_the_bar_against_the_reference_arithmetic(dev):
+    w = synth.WORKLOADS["ramp_field"]
+    sc = w.scene()
+    ps = w.poses(sc)
+    print(f"case agreement {w.name}: {len(ps)} envs", flush=True)
+    lid = vision.GpuLidar.from_grid(sc.sdf, sc.mins, sc.cell, width=w.width, height=w.height,
+                                    range_units=w.range_units, near_range=w.near_range,
+                                    max_steps=w.max_steps, hit_eps=w.hit_eps,
+                                    grid_dtype=torch.float32, device=dev)
+    img = lid.render(torch.as_tensor(ps.origin, device=dev), torch.as_tensor(ps.yaw, device=dev),
+                     torch.as_tensor(ps.pitch, device=dev),
+                     torch.as_tensor(ps.ducked, device=dev)).cpu().numpy()
+    kw = dict(width=w.width, height=w.height, range_units=w.range_units,
+              near_range=w.near_range, hit_eps=w.hit_eps, max_steps=w.max_steps)
+    torch.set_num_threads(max(1, min(16, len(os.sched_getaffinity(0)))))
+    keep = {}
+    ref = lockstep.render(sc.sdf, sc.mins, sc.cell, ps.origin, ps.yaw, ps.pitch, ps.ducked,
+                          keep=keep, **kw)
+    a = agreement.compare(sc.sdf, sc.mins, sc.cell, ps.origin, ps.yaw, ps.pitch, ps.ducked,
+                          img, ref, keep, list_max=None, **kw)
+    print({k: v for k, v in a.items() if k != "listed"}, flush=True)
+    assert a["rays"] == 2048 * 64 * 128
+    assert a["within_tol"] >= 0.999 and a["exact"] >= 0.999, a
+    assert a["renderer_differs"] == 0 and a["ref_retrace_differs"] == 0
+    assert a["outliers_other"] == 0, [o for o in a["listed"] if o["class"] == "other"]
+    assert a["outliers"] == len(a["listed"]) == (a["outliers_grazing"] + a["outliers_step_phase"]
+                                                 + a["outliers_tie_other"])
+    assert np.isfinite(img).all()
