@@ -55,14 +55,27 @@ _TILE_ORDERS = {"launch": _sdfr.ORDER_LAUNCH, "lookahead": _sdfr.ORDER_LOOKAHEAD
 _BORDER_FACES = {"auto": _sdfr.FACES_AUTO, "on": _sdfr.FACES_ON, "off": _sdfr.FACES_OFF}
 
 
+# The grid geometry is computed in the dtype the map core returns its bounds
+# in (float32 from the C core, core.py:869-878), as the reference computes it;
+# widening the bounds first would move mins, and every origin handed back to
+# the core's occupancy sampling, by up to half a float32 ulp.
+def _bounds(core):
+    mn, mx = core.map_bounds()
+    return np.asarray(mn), np.asarray(mx)
+
+
 def pick_cell(core, budget_voxels: float = 700e6) -> float:
     """Smallest power-of-two voxel size from 16 u whose padded grid fits the
-    voxel budget (the reference's rule, vision.py:283-298)."""
-    mn, mx = (np.asarray(v, np.float64) for v in core.map_bounds())
+    voxel budget (the reference's rule, vision.py:283-298): per axis the
+    padded extent over the cell, rounded up, multiplied axis by axis from
+    1.0 — all in the bounds' dtype, as there."""
+    mn, mx = _bounds(core)
     cell = 16.0
     while cell < 256.0:
-        ext = (mx - mn) + 2.0 * (4.0 * cell)
-        if float(np.prod(np.ceil(ext / cell))) <= budget_voxels:
+        voxels = 1.0
+        for n_axis in np.ceil(((mx - mn) + 2.0 * (4.0 * cell)) / cell):
+            voxels *= n_axis
+        if voxels <= budget_voxels:
             break
         cell *= 2.0
     return cell
@@ -70,10 +83,12 @@ def pick_cell(core, budget_voxels: float = 700e6) -> float:
 
 def grid_dims(core, cell: float):
     """(mins float64 (3,), nx, ny, nz): the map bounds padded by 4 cells and
-    cut into whole voxels (vision.py:310-322)."""
-    mn, mx = (np.asarray(v, np.float64) for v in core.map_bounds())
+    cut into whole voxels (vision.py:310-322). The padded minimum is taken in
+    the bounds' dtype and then widened to float64; the far side is padded in
+    the bounds' dtype too and measured from that float64 minimum."""
+    mn, mx = _bounds(core)
     pad = 4.0 * cell
-    mins = mn - pad
+    mins = (mn - pad).astype(np.float64)
     nx, ny, nz = (int(np.ceil(e / cell)) for e in (mx + pad) - mins)
     return mins, nx, ny, nz
 
