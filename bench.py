@@ -253,48 +253,45 @@ def bench_bake(args, w, dev):
     print(json.dumps(res), flush=True)
 
 
-def _reference_goal_sweeps_torch(occ_dev, cell, lo, hi):
-    """The reference's goal-field bake loop (goalfield.py:232-270) as torch
-    ops on this GPU: 26 shifted add+minimum passes per sweep over the whole
-    grid, solids re-pinned each sweep, a float64 convergence probe every 64
-    sweeps, at most 8000 sweeps. Returns (sweeps, seconds). A comparator for
-    the bake's speed, not a parity reference."""
-    import numpy as np
+def _reference_goal_loop_seconds(occ_dev, cell, lo, hi):
+    """Speed comparator for the goal-field bake: the reference's bake order
+    (goalfield.py:232-270) as torch ops on this GPU. Each sweep lowers every
+    free voxel to the smallest of its 26 neighbours plus cell * |offset|
+    (the neighbours read from a halo-padded copy made at the sweep's start)
+    and holds solids at +inf; the loop ends when the count of reached voxels
+    and their float64 sum repeat at a check every 64 sweeps, or after 8000
+    sweeps. Returns (sweeps, seconds). Not a parity reference."""
+    import itertools
     import torch
-    dev = occ_dev.device
-    solid = occ_dev != 0
-    nz, ny, nx = solid.shape
-    inf = float("inf")
-    dpad = torch.full((nz + 2, ny + 2, nx + 2), inf, device=dev)
-    d = torch.full((nz, ny, nx), inf, device=dev)
-    seed = torch.zeros_like(solid)
-    seed[lo[2]:hi[2] + 1, lo[1]:hi[1] + 1, lo[0]:hi[0] + 1] = True
-    seed &= ~solid
-    d[seed] = 0.0
-    del seed
-    offs = [(oz, oy, ox) for oz in (-1, 0, 1) for oy in (-1, 0, 1) for ox in (-1, 0, 1)
-            if (oz, oy, ox) != (0, 0, 0)]
-    wts = [cell * float(np.sqrt(oz * oz + oy * oy + ox * ox)) for oz, oy, ox in offs]
-    scratch = torch.empty_like(d)
+    blocked = occ_dev != 0
+    shape = tuple(blocked.shape)
+    field = torch.full(shape, math.inf, device=occ_dev.device)
+    box = tuple(slice(lo[a], hi[a] + 1) for a in (2, 1, 0))
+    field[box] = torch.where(blocked[box], math.inf, 0.0)
+    halo = torch.full(tuple(n + 2 for n in shape), math.inf, device=occ_dev.device)
+    moves = []
+    for off in itertools.product((-1, 0, 1), repeat=3):
+        if any(off):
+            view = halo[tuple(slice(1 + o, 1 + o + n) for o, n in zip(off, shape))]
+            moves.append((view, cell * math.sqrt(sum(o * o for o in off))))
+    cand = torch.empty_like(field)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    prev, it = None, 0
-    while it < 8000:
-        dpad[1:-1, 1:-1, 1:-1].copy_(d)
-        for (oz, oy, ox), wt in zip(offs, wts):
-            torch.add(dpad[1 + oz:1 + oz + nz, 1 + oy:1 + oy + ny, 1 + ox:1 + ox + nx], wt,
-                      out=scratch)
-            torch.minimum(d, scratch, out=d)
-        d.masked_fill_(solid, inf)
-        it += 1
-        if it % 64 == 0:
-            fin = torch.isfinite(d)
-            cur = (int(fin.sum()), float(d[fin].sum(dtype=torch.float64)))
-            if cur == prev:
+    sweeps, last = 0, None
+    while sweeps < 8000:
+        halo[1:-1, 1:-1, 1:-1].copy_(field)
+        for view, cost in moves:
+            torch.minimum(field, torch.add(view, cost, out=cand), out=field)
+        field.masked_fill_(blocked, math.inf)
+        sweeps += 1
+        if sweeps % 64 == 0:
+            reached = field[torch.isfinite(field)]
+            probe = (reached.numel(), float(reached.sum(dtype=torch.float64)))
+            if probe == last:
                 break
-            prev = cur
+            last = probe
     torch.cuda.synchronize()
-    return it, time.perf_counter() - t0
+    return sweeps, time.perf_counter() - t0
 
 
 def bench_goal(args, dev):
@@ -361,7 +358,7 @@ def bench_goal(args, dev):
            "reference_torch_gpu": None, "cpu_baseline": None}
     if not args.no_ref and w.occ.size <= 64 * 1024 * 1024:
         _log("[bench] the reference's torch sweep loop on this GPU ...")
-        sweeps, sec = _reference_goal_sweeps_torch(occ_dev, w.cell, lo, hi)
+        sweeps, sec = _reference_goal_loop_seconds(occ_dev, w.cell, lo, hi)
         res["reference_torch_gpu"] = {"value": round(sec * 1e3, 1), "unit": "ms", "sweeps": sweeps,
                                       "sample": "goalfield.py:232-270 loop as torch ops on "
                                                 "this GPU, one run"}

@@ -346,10 +346,11 @@ class GpuLidar:
         sdf = np.asarray(sdf)
         if sdf.ndim != 3:
             raise ValueError(f"the grid must be [nz, ny, nx], got shape {sdf.shape}")
-        # flat grid + integer strides, the reference's attributes (vision.py:476-480);
-        # an r16 copy is encoded from the fp32 values
+        # the flat device grid the handle's copy is made from (an r16 copy is
+        # encoded from the fp32 values); the handle keeps only its own
+        # re-laid-out copy, and sdf_flat reads the stored values back on demand
         flat_dtype = torch.float32 if grid_dtype == "r16" else grid_dtype
-        self.sdf_flat = torch.as_tensor(sdf, device=self.device).to(flat_dtype).reshape(-1)
+        flat = torch.as_tensor(sdf, device=self.device).to(flat_dtype).reshape(-1)
         self.nz, self.ny, self.nx = (int(v) for v in sdf.shape)
         self.stride_z = self.ny * self.nx
         self.stride_y = self.nx
@@ -409,9 +410,12 @@ class GpuLidar:
         err = ctypes.create_string_buffer(512)
         with torch.cuda.device(self.device):
             stream = torch.cuda.current_stream(self.device)
-            h = self._lib.sdfr_grid_create(ctypes.byref(desc), self.sdf_flat.data_ptr(),
+            h = self._lib.sdfr_grid_create(ctypes.byref(desc), flat.data_ptr(),
                                            _GRID_DTYPES[flat_dtype], 1, _GRID_DTYPES[grid_dtype],
                                            _LAYOUTS[layout], stream.cuda_stream, err, len(err))
+        # released to torch's pool on the stream the copy was enqueued on, so
+        # nothing reuses it before the copy has run
+        del flat
         if not h:
             raise _sdfr.SdfrError(err.value.decode("utf-8", "replace"))
         self._grid = h
@@ -707,6 +711,19 @@ class GpuLidar:
     def _dirs_pinhole(self, N, yaw_deg, pitch_deg, d2r):
         """Tangent-plane directions into ``_dx/_dy/_dz`` (vision.py:609-624)."""
         self._dirs_into(N, yaw_deg, pitch_deg, d2r, True)
+
+    @property
+    def sdf_flat(self) -> torch.Tensor:
+        """The reference's flat device grid (vision.py:476-480): the values
+        the march samples, [nz*ny*nx] in the store's dtype (fp32 holding the
+        decoded values for r16). It is read back from the handle's copy on
+        first access and kept; a lidar nobody asks holds only that copy."""
+        t = self.__dict__.get("_sdf_flat")
+        if t is None:
+            dt = torch.float32 if self.grid_dtype == "r16" else self.grid_dtype
+            t = self.stored_grid().to(dt).reshape(-1)
+            self._sdf_flat = t
+        return t
 
     @torch.no_grad()
     def stored_grid(self) -> torch.Tensor:

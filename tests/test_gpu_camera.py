@@ -142,8 +142,11 @@ def test_the_pinhole_flag_allocates_only_its_tables(dev, shelf):
     on = vision.GpuLidar.from_grid(shelf, np.zeros(3), CELL, width=8, height=4, pinhole=True,
                                    device=dev)
     base = {k for k, v in vars(off).items() if torch.is_tensor(v)}
-    assert base == {"sdf_flat", "mins", "yoff", "poff"}
+    # sdf_flat is read back from the handle's copy on first access
+    assert base == {"mins", "yoff", "poff"}
     assert {k for k, v in vars(on).items() if torch.is_tensor(v)} - base == {"uoff", "voff"}
+    assert torch.equal(off.sdf_flat.cpu(), torch.as_tensor(shelf, dtype=torch.float16).reshape(-1))
+    assert {k for k, v in vars(off).items() if torch.is_tensor(v)} == base | {"_sdf_flat"}
     assert off.pinhole is False and on.pinhole is True
     th, tv = np.tan(np.radians(60.0)), np.tan(np.radians(45.0))
     assert np.allclose(on.uoff.cpu().numpy(), th * (2 * np.arange(8) / 7 - 1), atol=1e-6)
@@ -152,6 +155,22 @@ def test_the_pinhole_flag_allocates_only_its_tables(dev, shelf):
             (np.array([[300.0, 600.0, 300.0]], np.float32), np.zeros(1, np.float32),
              np.array([-20.0], np.float32), np.zeros(1, np.float32))]
     assert off.render(*args).shape == (1, 4, 8) and on.render(*args).shape == (1, 4, 8)
+
+
+def test_the_lidar_holds_one_device_copy_of_the_grid(dev):
+    """Only the handle's re-laid-out copy stays resident: the flat grid the
+    copy is made from is released, and torch holds just the small tables
+    until sdf_flat is first read, which then equals the grid as stored."""
+    g = (np.random.default_rng(3).random((64, 128, 128), dtype=np.float32) * 100.0)
+    torch.cuda.synchronize(dev)
+    base = torch.cuda.memory_allocated(dev)
+    lid = vision.GpuLidar.from_grid(g, np.zeros(3), CELL, width=8, height=4,
+                                    grid_dtype=torch.float32, device=dev)
+    torch.cuda.synchronize(dev)
+    assert torch.cuda.memory_allocated(dev) - base < 64 * 1024
+    assert lid.grid_bytes >= g.nbytes
+    assert torch.equal(lid.sdf_flat.cpu(), torch.as_tensor(g).reshape(-1))
+    assert torch.cuda.memory_allocated(dev) - base >= g.nbytes   # now kept
 
 
 @pytest.mark.parametrize("W,H", [(1, 9), (9, 1), (1, 1)])

@@ -140,8 +140,9 @@ def test_grids_without_the_single_rounding_index(dev, cell, mins, gdt, store, la
 
 @pytest.mark.parametrize("eps", [16.0, 16.003, 0.0, -3.0, 70000.0, 1e-6, float("inf")])
 def test_fp16_samples_against_hit_eps_at_every_rounding(dev, eps):
-    """fp16 bricks compare each sample with hit_eps without converting it
-    (against the largest fp16 value <= hit_eps). Grid values at and a few
+    """fp16 bricks widen each sample to fp32 and compare it with hit_eps,
+    as the reference compares its fp16 gathers (vision.py:107-109). Grid
+    values at and a few
     fp16 steps either side of hit_eps (and of its fp16 floor), with hit_eps
     exact in fp16, between two fp16 values, zero, negative, beyond the fp16
     range and infinite: every image equals the oracle's on the f16-rounded
