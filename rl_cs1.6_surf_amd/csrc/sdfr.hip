@@ -267,6 +267,9 @@ template <typename GT>
 constexpr bool kPackStore = (std::is_same<GT, __half>::value && SDFR_F16_PACK) ||
                             (std::is_same<GT, R16>::value && SDFR_R16_PACK);
 
+// The record count is the descriptor's unsigned 32-bit byte range; the
+// builtin takes it as an int, and the cast keeps its bits, so a copy of up to
+// 4 GiB - 1 is addressed whole (offsets are unsigned 32-bit throughout).
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, (int)bytes, kRsrcWord3);
 }
@@ -1762,7 +1765,23 @@ constexpr int kMaxDevices = 64;
 std::mutex g_scratch_mu;
 void* g_scratch_ptr[kMaxDevices];
 
-// The current device's copy of `scratch`, looked up once per device.
+// The copy of `scratch` on device `dev` (the current device), looked up once
+// per device: by the first sdfr_grid_create on it, which allocates anyway and
+// so never runs inside a graph capture, or else by the first allocation-free
+// render there.
+hipError_t lookup_scratch(int dev, void** out) {
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_ptr[dev]) {
+        void* p = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess) return e;
+        if (!p) return hipErrorInvalidSymbol;
+        g_scratch_ptr[dev] = p;
+    }
+    *out = g_scratch_ptr[dev];
+    return hipSuccess;
+}
+
 int32_t scratch_for_current_device(const char* fn, const SdfrGrid* grid, void** out) {
     int dev = -1;
     hipError_t e = hipGetDevice(&dev);
@@ -1771,15 +1790,9 @@ int32_t scratch_for_current_device(const char* fn, const SdfrGrid* grid, void** 
         return fail(-2, "%s: the grid lives on device %d but device %d is current", fn,
                     grid->device, dev);
     if (dev < 0 || dev >= kMaxDevices) return fail(-2, "%s: device %d out of range", fn, dev);
-    std::lock_guard<std::mutex> lock(g_scratch_mu);
-    if (!g_scratch_ptr[dev]) {
-        void* p = nullptr;
-        e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
-        if (e != hipSuccess || !p)
-            return fail(-4, "%s: hipGetSymbolAddress(scratch) failed: %s", fn, hipGetErrorString(e));
-        g_scratch_ptr[dev] = p;
-    }
-    *out = g_scratch_ptr[dev];
+    e = lookup_scratch(dev, out);
+    if (e != hipSuccess)
+        return fail(-4, "%s: hipGetSymbolAddress(scratch) failed: %s", fn, hipGetErrorString(e));
     return 0;
 }
 
@@ -2031,6 +2044,12 @@ SDFR_API SdfrGrid* sdfr_grid_create(const SdfrGridDesc* desc, const void* src, i
         if (g->order_hist) (void)hipFree(g->order_hist);
         delete g;
         return nullptr;
+    }
+    // the allocation-free render's scratch on this device: looked up here,
+    // outside any capture; a failure is reported by that render's own lookup
+    if (g->device >= 0 && g->device < kMaxDevices) {
+        void* p = nullptr;
+        (void)lookup_scratch(g->device, &p);
     }
     return g;
 }

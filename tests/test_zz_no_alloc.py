@@ -162,3 +162,46 @@ def test_noalloc_captures_with_allocations_forbidden(dev):
             torch.cuda.synchronize()
     finally:
         h.close()
+
+
+_FIRST_CALL_IN_CAPTURE = r"""
+import sys
+sys.path[:0] = sys.argv[1:4]
+import torch
+import test_zz_no_alloc as t
+from surfgym import _sdfr
+dev = torch.device("cuda:0")
+h = t._Handle(dev, "small_ramps")
+poses, keep = h.poses(dev, 16)
+want = torch.empty(16, h.w.height, h.w.width, device=dev)
+h.render(dev, poses, want)
+out = torch.full_like(want, -1.0)
+g = torch.cuda.CUDAGraph()
+with torch.cuda.graph(g, capture_error_mode="global"):
+    rc = h.render_noalloc(dev, poses, out)
+assert rc == 0, _sdfr.last_error()
+for i in range(3):
+    out.fill_(-1.0)
+    g.replay()
+    torch.cuda.synchronize()
+    assert torch.equal(out, want), i
+h.close()
+print("first call captured and replayed", flush=True)
+"""
+
+
+def test_the_first_noalloc_call_can_be_a_captured_one():
+    """In a fresh process, whose first sdfr_render_noalloc call is made inside
+    a global-mode graph capture: the scratch address was looked up when the
+    grid was created, so the captured call makes no runtime call a capture
+    forbids, and every replay equals sdfr_render's image."""
+    import subprocess
+    import sys
+    from pathlib import Path
+    here = Path(__file__).resolve().parent
+    print("case noalloc first call inside a capture (child process)", flush=True)
+    r = subprocess.run([sys.executable, "-c", _FIRST_CALL_IN_CAPTURE, str(here),
+                        str(here.parent), str(here.parent / "rl_cs1.6_surf_amd")],
+                       capture_output=True, text=True, timeout=300)
+    assert r.returncode == 0, r.stdout[-2000:] + r.stderr[-2000:]
+    assert "first call captured and replayed" in r.stdout
