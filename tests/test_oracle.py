@@ -353,3 +353,85 @@ def test_bake_matches_brute_force_on_tiny_grids():
     shell = np.minimum.reduce([x + 1, 5 - x, y + 1, 4 - y, z + 1, 3 - z]) * 16.0
     assert np.array_equal(d, shell)
     assert edt.stored(d).dtype == np.float32
+
+
+# ------------------------------------------------------------ surf-mask channel --
+def test_surf_channel_closed_form_on_a_floor():
+    """The second channel is |n_z| of the voxel the march stopped in, read at
+    the clamped depth (vision.py:176-187, :658-665). Floor slab, |n_z| grid
+    127 in the solid layers and 0 in the air: every ray that stops on the
+    floor reads exactly 1.0 (127 / 127), every ray that runs out to the
+    range reads the air's 0, and the depth channel equals the depth-only
+    render bit for bit."""
+    cell = 16.0
+    nz = 16
+    g = np.maximum((np.arange(nz, dtype=np.float32) - 3.0) * cell, 0.0)[:, None, None] \
+        * np.ones((1, 32, 32), np.float32)                    # solid for iz <= 3
+    snz = np.where(g == 0.0, 127, 0).astype(np.int8)
+    origin = np.array([[256.0, 256.0, 150.0], [100.0, 400.0, 180.0]], np.float32)
+    yaw = np.array([10.0, -140.0], np.float32)
+    pitch = np.array([-30.0, 5.0], np.float32)
+    duck = np.zeros(2, np.float32)
+    kw = dict(width=32, height=16, range_units=1500.0, near_range=1500.0, max_steps=200)
+    both, loads = oracle.render(g, np.zeros(3, np.float32), cell, origin, yaw, pitch, duck,
+                                surf_nz=snz, **kw)
+    depth, _ = oracle.render(g, np.zeros(3, np.float32), cell, origin, yaw, pitch, duck, **kw)
+    assert both.shape == (2, 16, 32, 2)
+    assert np.array_equal(both[..., 0], depth)
+    hit = both[..., 0] < 1.0
+    assert 0.2 < hit.mean() < 0.9
+    assert np.all(both[..., 1][hit] == 1.0)
+    assert np.all(both[..., 1][~hit] == 0.0)
+
+
+def test_surf_channel_reads_the_stop_voxel_of_each_ray():
+    """On a ramp scene with a distinct |n_z| code per voxel, each ray's
+    second channel is the code of the voxel its own march (the sample by
+    sample trace) stopped in, divided by 127 in fp32 as the CPU path does
+    (``snz.float() / 127.0``). For a hit that is the last voxel sampled; for
+    a ray clamped to the range it is the voxel at the range point. Reading
+    the voxel of the sample before the stop (a plausible slip) disagrees on
+    most hits."""
+    from oracle import agreement
+    from surfgym import synth
+    w = synth.WORKLOADS["small_ramps"]
+    sc = w.scene()
+    ps = w.poses(sc, 3)
+    rng = np.random.default_rng(11)
+    snz = rng.integers(0, 128, sc.sdf.shape).astype(np.int8)
+    kw = dict(width=w.width, height=w.height, range_units=w.range_units,
+              near_range=w.near_range, hit_eps=w.hit_eps, max_steps=w.max_steps)
+    img, _ = oracle.render(sc.sdf, sc.mins, sc.cell, ps.origin, ps.yaw, ps.pitch, ps.ducked,
+                           surf_nz=snz, **kw)
+    lib = oracle._load()
+    mins = np.asarray(sc.mins, np.float32)
+    inv = F32(1.0 / sc.cell)
+    nz, ny, nx = sc.sdf.shape
+    hits = slips = 0
+    for e in range(3):
+        eye = (F32(ps.origin[e, 0]), F32(ps.origin[e, 1]),
+               F32(F32(ps.origin[e, 2]) + F32(12.0 if ps.ducked[e] else 17.0)))
+        for r in range(0, w.height, 3):
+            for c in range(0, w.width, 5):
+                d = np.empty(3, np.float32)
+                lib.oracle_ray_dir(0, r, c, w.width, w.height, 120.0, 90.0, 0.0, 0.0,
+                                   float(ps.yaw[e]), float(ps.pitch[e]),
+                                   d.ctypes.data_as(oracle.ctypes.c_void_p))
+                tr = agreement.trace(sc.sdf, mins, sc.cell, eye, d,
+                                     range_units=w.range_units, hit_eps=w.hit_eps,
+                                     min_step=float(F32(0.3 * sc.cell)), max_steps=w.max_steps)
+                if tr["why"] == "hit":
+                    ix, iy, iz = tr["vox"][-1]
+                    hits += 1
+                    px, py, pz = tr["vox"][-2] if len(tr["vox"]) > 1 else tr["vox"][-1]
+                    slips += snz[pz, py, px] != snz[iz, iy, ix]
+                else:
+                    t = min(F32(tr["t"]), F32(w.range_units))
+                    idx = []
+                    for a, n in ((0, nx), (1, ny), (2, nz)):
+                        f = F32(F32(F32(eye[a] + F32(d[a] * t)) - mins[a]) * inv)
+                        idx.append(0 if not f > 0 else min(int(f), n - 1))
+                    ix, iy, iz = idx
+                assert img[e, r, c, 1] == F32(snz[iz, iy, ix]) / F32(127.0), (e, r, c, tr["why"])
+    assert hits > 50
+    assert slips > 0.5 * hits
