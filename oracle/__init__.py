@@ -27,9 +27,13 @@ its goal field:
 Where each is pinned (closed forms, invariants, brute force on tiny inputs,
 an independent second implementation, planted mistakes):
 
-* render, ray_dirs, offsets, encode — tests/test_oracle.py and the committed
-  fixtures in tests/golden/ (tests/test_golden.py);
+* render (the surf-mask channel included), ray_dirs, offsets, encode —
+  tests/test_oracle.py and the committed fixtures in tests/golden/
+  (tests/test_golden.py);
 * lockstep — tests/test_oracle_lockstep.py, against render;
+* agreement — tests/test_oracle_lockstep.py: the grazing angle against a
+  floor and a wall in closed form, each outlier's re-trace reproducing both
+  renders, and planted mistakes (a yaw offset, corrupted pixels) caught;
 * r16_encode / r16_decode — tests/test_oracle_store.py;
 * edt — tests/test_oracle.py (exhaustive nearest-solid search);
 * goal — tests/test_oracle_goal.py.
