@@ -112,9 +112,10 @@ def _last_step(tr):
 def compare(grid, mins, cell, origin, yaw_deg, pitch_deg, ducked, image, ref_enc, ref_keep, *,
             width, height, range_units, near_range, hit_eps, max_steps, min_step=None,
             hfov_deg=120.0, vfov_deg=90.0, list_max=64):
-    """Agreement of ``image`` (the renderer's (N,H,W) f32 encodings) with
-    ``ref_enc`` (the lockstep render's, same inputs) whose per-ray depths and
-    directions are in ``ref_keep`` (lockstep.render(..., keep=...)).
+    """Agreement of ``image`` (the renderer's (N,H,W) f32 encodings of an
+    equiangular camera, the lockstep's only one) with ``ref_enc`` (the
+    lockstep render's, same inputs) whose per-ray depths and directions are
+    in ``ref_keep`` (lockstep.render(..., keep=...)).
 
     Returns a dict: rays, exact (fraction of bit-identical encodings),
     within_tol (fraction within 0.5 u and 1e-3), outliers (count) and their
