@@ -47,7 +47,7 @@ def cpu_baseline(w, sc, envs, repeats=5, image=None):
     With ``image`` (the GPU render of the same ``envs`` poses, (N,H,W) f32)
     it also reports ``agreement``: one more lockstep render, untimed, that
     keeps its per-ray depths and directions, compared ray by ray with the
-    GPU image at the north star's tolerance (0.5 u in depth, 1e-3 in the
+    GPU image at the accuracy bar (0.5 u in depth, 1e-3 in the
     encoding), every ray outside it re-traced and classified
     (oracle/agreement.py)."""
     import torch

@@ -13,7 +13,7 @@ its goal field:
 * :mod:`oracle.goal` — the goal-field bake and sampler
   (python/surfgym/goalfield.py), ``oracle/goal.c``.
 * :mod:`oracle.agreement` — a render compared with the lockstep render
-  (the reference's CPU arithmetic) at the north star's tolerance, every
+  (the reference's CPU arithmetic) at the accuracy bar (0.5 u, 1e-3), every
   ray outside it re-traced and classified.
 * :mod:`oracle.lockstep` — the reference's CPU fallback shape
   (``_render_torch``, vision.py:626-666): torch tensors over all rays in

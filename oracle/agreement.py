@@ -7,8 +7,8 @@ CPU kernels; ``oracle/lockstep.py`` restates it with those same torch calls.
 The renderer (and ``oracle/march.c``, which it equals bit for bit) takes
 them correctly rounded. The two can therefore differ in the last bit of a
 ray direction, and a sample that lies within that much of a voxel face then
-reads the neighbouring voxel. :func:`compare` measures the north star's
-tolerance on a whole image pair — a ray agrees when its depth is within
+reads the neighbouring voxel. :func:`compare` measures the renderer's
+accuracy bar on a whole image pair — a ray agrees when its depth is within
 0.5 u of the reference's and its encoding within 1e-3 — and classifies
 every ray that does not:
 

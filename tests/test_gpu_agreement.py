@@ -4,7 +4,7 @@ The reference's CPU render (python/surfgym/vision.py:596-657) takes cos/sin/
 exp from torch's CPU kernels; oracle/lockstep.py restates it with those same
 calls. This renders all 2048 ramp_field envs (16.8 M rays) on the GPU, the
 same poses through the lockstep on this host's cores, and holds the pair to
-the north star's bar: >= 99.9% of rays within 0.5 u of the reference's depth
+the accuracy bar: >= 99.9% of rays within 0.5 u of the reference's depth
 and 1e-3 of its encoding, every ray outside it classified by
 oracle/agreement.py, and every outlier's GPU value reproduced by the
 oracle's march. None may be unexplained (class "other": two marches that part

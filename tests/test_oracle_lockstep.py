@@ -66,7 +66,7 @@ def _agreement(name, n, *, yaw_shift=0.0, corrupt=0):
 
 
 def test_agreement_with_the_reference_arithmetic_at_256_envs():
-    """The north star's bar against the reference's own CPU arithmetic
+    """The accuracy bar against the reference's own CPU arithmetic
     (torch's cos/sin/exp, vision.py:596-657) on 256 ramp_field envs (2.1 M
     rays): >= 99.9% of rays within 0.5 u and 1e-3, and every ray outside
     that is classified — a grazing hit, or two hits of the same surface one
