@@ -254,8 +254,11 @@ SDFR_API int32_t sdfr_render(const SdfrGrid* grid, const SdfrCam* cam,
  * renders whose sdfr_workspace_bytes() exceed it are refused (-2) before any
  * launch. Every call on one GPU shares that GPU's array: calls that overlap
  * on one GPU (other streams, other threads, other handles) race and must be
- * serialised by the caller. The grid's device must be current. Otherwise as
- * sdfr_render: asynchronous on `stream`, 0 or < 0 with sdfr_last_error(). */
+ * serialised by the caller. The grid's device must be current. The array's
+ * address on a device is looked up by the first sdfr_grid_create there, so
+ * a process's very first call may already be inside a graph capture.
+ * Otherwise as sdfr_render: asynchronous on `stream`, 0 or < 0 with
+ * sdfr_last_error(). */
 SDFR_API int32_t sdfr_render_noalloc(const SdfrGrid* grid, const SdfrCam* cam,
                                      const SdfrPoses* poses, const SdfrImage* image,
                                      void* stream);
