@@ -413,8 +413,8 @@ class GpuLidar:
             h = self._lib.sdfr_grid_create(ctypes.byref(desc), flat.data_ptr(),
                                            _GRID_DTYPES[flat_dtype], 1, _GRID_DTYPES[grid_dtype],
                                            _LAYOUTS[layout], stream.cuda_stream, err, len(err))
-        # released to torch's pool on the stream the copy was enqueued on, so
-        # nothing reuses it before the copy has run
+        # sdfr_grid_create has finished reading it when it returns (it waits
+        # for its stream), so the flat grid can go back to torch's pool
         del flat
         if not h:
             raise _sdfr.SdfrError(err.value.decode("utf-8", "replace"))
