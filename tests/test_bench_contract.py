@@ -121,3 +121,32 @@ def test_step_census_statistics_on_a_known_tally():
     assert c["loads_mean"] == round((45 + 550) / 64, 3)
     # one 16x4 tile whose slowest ray takes 10 steps
     assert c["lane_efficiency_per_tile"] == round(595 / 640, 4)
+
+
+def test_cpu_baseline_reports_its_agreement_with_the_render():
+    """The CPU leg times the lockstep render and, given the GPU image of the
+    same envs, reports the agreement record the JSON line carries. Here the
+    oracle's image stands in for the GPU's (equal bit for bit on the GPU):
+    on small_ramps the two arithmetics agree on every ray; a planted wrong
+    pixel is caught as an image that is not the oracle's march."""
+    import oracle
+    from surfgym import synth
+    w = synth.WORKLOADS["small_ramps"]
+    sc = w.scene()
+    ps = w.poses(sc, 16)
+    img, _ = oracle.render(sc.sdf, sc.mins, sc.cell, ps.origin, ps.yaw, ps.pitch, ps.ducked,
+                           width=w.width, height=w.height, range_units=w.range_units,
+                           near_range=w.near_range, hit_eps=w.hit_eps, max_steps=w.max_steps)
+    r = bench.cpu_baseline(w, sc, 16, repeats=1, image=img)
+    a = r["agreement"]
+    assert r["kind"] == "port" and r["cores"] >= 1 and r["value"] > 0
+    for key in ("rays", "exact", "within_tol", "outliers", "outliers_grazing",
+                "outliers_step_phase", "outliers_tie_other", "outliers_other",
+                "renderer_differs", "not_step_phase"):
+        assert key in a, key
+    assert a["rays"] == 16 * 64 * 128 and a["exact"] == 1.0 and a["outliers"] == 0
+    bad = img.copy()
+    bad[3, 10, 20] = 0.123
+    a = bench.cpu_baseline(w, sc, 16, repeats=1, image=bad)["agreement"]
+    assert a["renderer_differs"] == 1 and a["outliers"] == 1
+    assert bench.cpu_baseline(w, sc, 16, repeats=1)["agreement"] is None
