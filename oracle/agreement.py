@@ -56,11 +56,27 @@ ENC_TOL = 1e-3
 WHY = ("hit", "range", "exhausted")
 
 
-def _dir(lib, width, height, hfov, vfov, yaw, pitch, r, c):
+def _dir(lib, width, height, hfov, vfov, yaw, pitch, r, c, pinhole=False):
     d = np.empty(3, np.float32)
-    lib.oracle_ray_dir(0, int(r), int(c), int(width), int(height), float(hfov), float(vfov),
-                       0.0, 0.0, float(yaw), float(pitch), _ptr(d))
+    tan_h = float(np.tan(0.5 * hfov * (np.pi / 180.0)))
+    tan_v = float(np.tan(0.5 * vfov * (np.pi / 180.0)))
+    lib.oracle_ray_dir(1 if pinhole else 0, int(r), int(c), int(width), int(height), float(hfov),
+                       float(vfov), tan_h, tan_v, float(yaw), float(pitch), _ptr(d))
     return d
+
+
+def _stop_voxel(eye, d, t, mins, cell, shape):
+    """The voxel under depth t along d (the surf channel's index, vision.py:
+    658-665) in fp32, and each axis's voxel coordinate."""
+    f = np.float32
+    inv = f(1.0 / float(cell))
+    nz, ny, nx = shape
+    idx, pos = [], []
+    for a, n in ((0, nx), (1, ny), (2, nz)):
+        q = f(f(f(eye[a]) + f(f(d[a]) * f(t))) - f(mins[a])) * inv
+        pos.append(float(q))
+        idx.append(0 if not q > 0 else min(int(q), n - 1))
+    return tuple(idx), pos
 
 
 def trace(grid, mins, cell, eye, d, *, range_units, hit_eps, min_step, max_steps):
@@ -111,11 +127,17 @@ def _last_step(tr):
 
 def compare(grid, mins, cell, origin, yaw_deg, pitch_deg, ducked, image, ref_enc, ref_keep, *,
             width, height, range_units, near_range, hit_eps, max_steps, min_step=None,
-            hfov_deg=120.0, vfov_deg=90.0, list_max=64):
-    """Agreement of ``image`` (the renderer's (N,H,W) f32 encodings of an
-    equiangular camera, the lockstep's only one) with ``ref_enc`` (the
-    lockstep render's, same inputs) whose per-ray depths and directions are
-    in ``ref_keep`` (lockstep.render(..., keep=...)).
+            hfov_deg=120.0, vfov_deg=90.0, list_max=64, pinhole=False, surf_nz=None):
+    """Agreement of ``image`` (the renderer's (N,H,W) f32 encodings, or
+    (N,H,W,2) with the surf channel and ``surf_nz``) with ``ref_enc`` (the
+    lockstep render's, same inputs and camera) whose per-ray depths and
+    directions are in ``ref_keep`` (lockstep.render(..., keep=...)).
+
+    With the surf channel, the rays whose depths agree but whose |n_z|
+    differ are counted separately: ``surf_tie`` when the two directions put
+    the depth's end point on either side of a voxel face within ``TIE_U``
+    (the same voxel-face tie, at the end of the march), ``surf_other``
+    otherwise.
 
     Returns a dict: rays, exact (fraction of bit-identical encodings),
     within_tol (fraction within 0.5 u and 1e-3), outliers (count) and their
@@ -123,10 +145,14 @@ def compare(grid, mins, cell, origin, yaw_deg, pitch_deg, ducked, image, ref_enc
     ``list_max`` outliers described (all of them when None)."""
     lib = _load()
     g = np.ascontiguousarray(grid, np.float32)
-    img = np.asarray(image, np.float32)
-    ref = np.asarray(ref_enc, np.float32)
-    if img.shape != ref.shape or img.ndim != 3:
-        raise ValueError(f"image shapes differ: {img.shape} vs {ref.shape}")
+    img_all = np.asarray(image, np.float32)
+    ref_all = np.asarray(ref_enc, np.float32)
+    surf = img_all.ndim == 4
+    if img_all.shape != ref_all.shape or img_all.ndim not in (3, 4) or surf != (surf_nz is not None):
+        raise ValueError(f"image shapes differ or the surf grid is missing: {img_all.shape} vs "
+                         f"{ref_all.shape}")
+    img = img_all[..., 0] if surf else img_all
+    ref = ref_all[..., 0] if surf else ref_all
     rng = float(range_units)
     near = float(near_range) if near_range else rng
     mstep = float(np.float32(0.3 * cell)) if min_step is None else float(min_step)
@@ -141,9 +167,10 @@ def compare(grid, mins, cell, origin, yaw_deg, pitch_deg, ducked, image, ref_enc
     classes = {"grazing": 0, "step_phase": 0, "tie_other": 0, "other": 0}
     listed, max_dt, max_de = [], 0.0, 0.0
     n_out = renderer_differs = ref_retrace_differs = 0
+    depth_out = set()
     for e, r, c in differ:
         eye = (org[e, 0], org[e, 1], np.float32(org[e, 2] + np.float32(12.0 if duck[e] else 17.0)))
-        d_o = _dir(lib, width, height, hfov_deg, vfov_deg, yaw[e], pitch[e], r, c)
+        d_o = _dir(lib, width, height, hfov_deg, vfov_deg, yaw[e], pitch[e], r, c, pinhole)
         d_t = ref_keep["dirs"][e, r, c]
         to = trace(g, mins, cell, eye, d_o, **kw)
         tt = trace(g, mins, cell, eye, d_t, **kw)
@@ -159,6 +186,7 @@ def compare(grid, mins, cell, origin, yaw_deg, pitch_deg, ducked, image, ref_enc
         if dt <= DEPTH_TOL_U and de <= ENC_TOL:
             continue
         n_out += 1
+        depth_out.add((int(e), int(r), int(c)))
         angles = [a for a in (_normal_angle(g, to, d_o) if to["why"] == "hit" else None,
                               _normal_angle(g, tt, d_t) if tt["why"] == "hit" else None)
                   if a is not None]
@@ -190,6 +218,35 @@ def compare(grid, mins, cell, origin, yaw_deg, pitch_deg, ducked, image, ref_enc
                            "angle_deg": round(max(angles), 1) if angles else None,
                            "last_step_u": round(last, 3), "split_step": k,
                            "split_face_u": split})
+    extra = {}
+    if surf:
+        snz = np.ascontiguousarray(surf_nz, np.int8)
+        sdiff = np.argwhere(img_all[..., 1] != ref_all[..., 1])
+        tie = other = with_depth = 0
+        for e, r, c in sdiff:
+            if (int(e), int(r), int(c)) in depth_out:
+                with_depth += 1
+                continue
+            eye = (org[e, 0], org[e, 1],
+                   np.float32(org[e, 2] + np.float32(12.0 if duck[e] else 17.0)))
+            d_o = _dir(lib, width, height, hfov_deg, vfov_deg, yaw[e], pitch[e], r, c, pinhole)
+            d_t = ref_keep["dirs"][e, r, c]
+            t_o = min(np.float32(trace(g, mins, cell, eye, d_o, **kw)["t"]), np.float32(rng))
+            t_t = ref_keep["t"][e, r, c]
+            vo, po = _stop_voxel(eye, d_o, t_o, mins, cell, g.shape)
+            vt, pt_ = _stop_voxel(eye, d_t, t_t, mins, cell, g.shape)
+            if np.float32(snz[vo[2], vo[1], vo[0]]) / np.float32(127.0) != img_all[e, r, c, 1]:
+                renderer_differs += 1
+            axes = [a for a in range(3) if vo[a] != vt[a]]
+            near_face = bool(axes) and all(
+                max(abs(q - round(q)) for q in (po[a], pt_[a])) * float(cell) <= TIE_U
+                for a in axes)
+            if near_face:
+                tie += 1
+            else:
+                other += 1
+        extra = {"surf_differs": int(len(sdiff)), "surf_with_depth_outlier": with_depth,
+                 "surf_tie": tie, "surf_other": other}
     return {"rays": rays, "exact": round(1.0 - len(differ) / rays, 7),
             "within_tol": round(1.0 - n_out / rays, 7), "outliers": n_out,
             "outliers_grazing": classes["grazing"], "outliers_step_phase": classes["step_phase"],
@@ -198,4 +255,4 @@ def compare(grid, mins, cell, origin, yaw_deg, pitch_deg, ducked, image, ref_enc
             "renderer_differs": renderer_differs, "ref_retrace_differs": ref_retrace_differs,
             "tolerance": f"depth within {DEPTH_TOL_U} u and encoding within {ENC_TOL}",
             "grazing": f"angle to the stop voxel's grid gradient above {GRAZING_DEG:g} deg",
-            "listed": listed}
+            **extra, "listed": listed}

@@ -27,11 +27,31 @@ def _equiangular_tables(width, height, hfov_deg, vfov_deg):
             torch.as_tensor(poff, dtype=torch.float32))
 
 
+def _pinhole_tables(width, height, hfov_deg, vfov_deg):
+    """Tangent-plane offsets of the pinhole camera (vision.py:515-529): the
+    outermost pixels on the fov edge, a one-pixel axis on the centre ray."""
+    d2r = np.pi / 180.0
+    tu = float(np.tan(0.5 * hfov_deg * d2r))
+    tv = float(np.tan(0.5 * vfov_deg * d2r))
+    uo = tu * (2.0 * np.arange(width) / max(width - 1, 1) - 1.0)
+    vo = tv * (1.0 - 2.0 * np.arange(height) / max(height - 1, 1))
+    if width == 1:
+        uo[:] = 0.0
+    if height == 1:
+        vo[:] = 0.0
+    return (torch.as_tensor(uo, dtype=torch.float32),
+            torch.as_tensor(vo, dtype=torch.float32))
+
+
 @torch.no_grad()
 def render(grid, mins, cell, origin, yaw_deg, pitch_deg, ducked, *, width=128, height=64,
            hfov_deg=120.0, vfov_deg=90.0, range_units=2000.0, near_range=None, hit_eps=None,
-           min_step=None, max_steps=64, env_chunk=64, keep=None):
-    """(N,H,W) f32 encodings, computed on the CPU with torch in lockstep.
+           min_step=None, max_steps=64, env_chunk=64, keep=None, pinhole=False, surf_nz=None):
+    """(N,H,W) f32 encodings, computed on the CPU with torch in lockstep;
+    (N,H,W,2) with ``surf_nz`` (the int8 |n_z|*127 grid): the encoding and
+    |n_z| of the voxel re-derived at the clamped depth, as a float divided by
+    127 (vision.py:658-666). ``pinhole`` casts the tangent-plane rays of
+    ``_dirs_pinhole`` (vision.py:609-624) instead of the equiangular ones.
 
     ``keep``: a dict that receives the march's own per-ray values, ``t``
     (N,H,W) f32 depths (clamped to the range) and ``dirs`` (N,H,W,3) f32
@@ -51,21 +71,41 @@ def render(grid, mins, cell, origin, yaw_deg, pitch_deg, ducked, *, width=128, h
     inv_cell = 1.0 / float(cell)
     d2r = np.pi / 180.0
     yoff, poff = _equiangular_tables(width, height, hfov_deg, vfov_deg)
+    uoff, voff = _pinhole_tables(width, height, hfov_deg, vfov_deg)
+    snz = None
+    if surf_nz is not None:
+        snz = torch.as_tensor(np.ascontiguousarray(surf_nz, np.int8)).reshape(-1)
     n_all = origin.shape[0]
-    out = torch.empty(n_all, height, width)
+    out = torch.empty((n_all, height, width) + ((2,) if snz is not None else ()))
     if keep is not None:
         keep["t"] = np.empty((n_all, height, width), np.float32)
         keep["dirs"] = np.empty((n_all, height, width, 3), np.float32)
     for a in range(0, n_all, env_chunk):
         b = min(n_all, a + env_chunk)
         n = b - a
-        # per-pixel angles (vision.py:603-607)
-        p = (pitch[a:b] * d2r).view(n, 1, 1) + poff.view(1, height, 1)
-        y = (yaw[a:b] * d2r).view(n, 1, 1) + yoff.view(1, 1, width)
-        cp = torch.cos(p)
-        dx = (cp * torch.cos(y)).reshape(-1)
-        dy = (cp * torch.sin(y)).reshape(-1)
-        dz = torch.sin(p).expand(n, height, width).reshape(-1)
+        if pinhole:
+            # forward + u*right + v*up, then times its rsqrt (vision.py:614-624)
+            yw = (yaw[a:b] * d2r).view(n, 1, 1)
+            pt = (pitch[a:b] * d2r).view(n, 1, 1)
+            cy, sy = torch.cos(yw), torch.sin(yw)
+            cp, sp = torch.cos(pt), torch.sin(pt)
+            u = uoff.view(1, 1, width)
+            v = voff.view(1, height, 1)
+            fx = cp * cy + u * sy - v * sp * cy
+            fy = cp * sy - u * cy - v * sp * sy
+            fz = sp + v * cp
+            inv = torch.rsqrt(fx * fx + fy * fy + fz * fz)
+            dx = (fx * inv).reshape(-1)
+            dy = (fy * inv).reshape(-1)
+            dz = (fz * inv).reshape(-1)
+        else:
+            # per-pixel angles (vision.py:603-607)
+            p = (pitch[a:b] * d2r).view(n, 1, 1) + poff.view(1, height, 1)
+            y = (yaw[a:b] * d2r).view(n, 1, 1) + yoff.view(1, 1, width)
+            cp = torch.cos(p)
+            dx = (cp * torch.cos(y)).reshape(-1)
+            dy = (cp * torch.sin(y)).reshape(-1)
+            dz = torch.sin(p).expand(n, height, width).reshape(-1)
         hw = height * width
         eye_z = origin[a:b, 2] + torch.where(duck[a:b], 12.0, 17.0)
         ex = origin[a:b, 0].repeat_interleave(hw)
@@ -88,5 +128,13 @@ def render(grid, mins, cell, origin, yaw_deg, pitch_deg, ducked, *, width=128, h
             keep["dirs"][a:b] = torch.stack((dx, dy, dz), 1).view(n, height, width, 3).numpy()
         enc = (torch.clamp(t, max=near) / near
                + 0.25 * (1.0 - torch.exp(-torch.clamp(t - near, min=0.0) / 2500.0)))
-        out[a:b] = enc.view(n, height, width)
+        if snz is None:
+            out[a:b] = enc.view(n, height, width)
+        else:
+            # the voxel under the clamped depth, by the march's own index formula
+            ix = ((ex + dx * t - mins_t[0]) * inv_cell).long().clamp_(0, nx - 1)
+            iy = ((ey + dy * t - mins_t[1]) * inv_cell).long().clamp_(0, ny - 1)
+            iz = ((ez + dz * t - mins_t[2]) * inv_cell).long().clamp_(0, nz - 1)
+            m = snz[(iz * ny + iy) * nx + ix].float() / 127.0
+            out[a:b] = torch.stack((enc, m), -1).view(n, height, width, 2)
     return out.numpy()

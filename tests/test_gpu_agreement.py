@@ -25,6 +25,51 @@ from surfgym import synth, vision
 pytestmark = pytest.mark.gpu
 
 
+def _nz_code_grid(sdf):
+    gz = np.gradient(sdf, axis=0)
+    gy = np.gradient(sdf, axis=1)
+    gx = np.gradient(sdf, axis=2)
+    nrm = np.sqrt(gx * gx + gy * gy + gz * gz)
+    return np.where(nrm > 0, np.rint(np.abs(gz) / np.maximum(nrm, 1e-9) * 127), 0).astype(np.int8)
+
+
+@pytest.mark.parametrize("variant", ["pinhole", "surf_mask"])
+def test_variant_renders_meet_the_bar_against_the_reference_arithmetic(dev, variant):
+    """The pinhole camera and the surf-mask channel at the headline size:
+    the GPU image against the lockstep render of the same variant
+    (``_dirs_pinhole`` with torch's trig and rsqrt; the |n_z| code under the
+    clamped depth over 127), every depth outlier classified, and every |n_z|
+    that differs where the depths agree explained by a voxel-face tie at the
+    march's end point."""
+    w = synth.WORKLOADS["ramp_field"]
+    sc = w.scene()
+    ps = w.poses(sc)
+    extra = dict(pinhole=True) if variant == "pinhole" else dict(surf_nz=_nz_code_grid(sc.sdf))
+    print(f"case agreement {w.name} {variant}: {len(ps)} envs", flush=True)
+    lid = vision.GpuLidar.from_grid(sc.sdf, sc.mins, sc.cell, width=w.width, height=w.height,
+                                    range_units=w.range_units, near_range=w.near_range,
+                                    max_steps=w.max_steps, hit_eps=w.hit_eps,
+                                    grid_dtype=torch.float32, device=dev, **extra)
+    img = lid.render(torch.as_tensor(ps.origin, device=dev), torch.as_tensor(ps.yaw, device=dev),
+                     torch.as_tensor(ps.pitch, device=dev),
+                     torch.as_tensor(ps.ducked, device=dev)).cpu().numpy()
+    kw = dict(width=w.width, height=w.height, range_units=w.range_units,
+              near_range=w.near_range, hit_eps=w.hit_eps, max_steps=w.max_steps)
+    torch.set_num_threads(max(1, min(16, len(os.sched_getaffinity(0)))))
+    keep = {}
+    ref = lockstep.render(sc.sdf, sc.mins, sc.cell, ps.origin, ps.yaw, ps.pitch, ps.ducked,
+                          keep=keep, **kw, **extra)
+    a = agreement.compare(sc.sdf, sc.mins, sc.cell, ps.origin, ps.yaw, ps.pitch, ps.ducked,
+                          img, ref, keep, list_max=None, **kw, **extra)
+    print({k: v for k, v in a.items() if k != "listed"}, flush=True)
+    assert a["within_tol"] >= 0.999 and a["exact"] >= 0.999, a
+    assert a["renderer_differs"] == 0 and a["ref_retrace_differs"] == 0
+    assert a["outliers_other"] == 0, [o for o in a["listed"] if o["class"] == "other"]
+    if variant == "surf_mask":
+        assert a["surf_other"] == 0, a
+        assert a["surf_differs"] == a["surf_with_depth_outlier"] + a["surf_tie"]
+
+
 def test_headline_render_meets_the_bar_against_the_reference_arithmetic(dev):
     w = synth.WORKLOADS["ramp_field"]
     sc = w.scene()

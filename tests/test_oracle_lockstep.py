@@ -181,3 +181,87 @@ def test_a_planted_mistake_in_the_lockstep_is_caught():
     b, _ = oracle.render(sc.sdf, sc.mins, sc.cell, ps.origin, ps.yaw, ps.pitch, ps.ducked,
                          threads=8, **kw)
     assert float((a == b).mean()) < 0.99
+
+
+def _nz_code_grid(sdf):
+    """|n_z| * 127 of the grid's own central-difference gradient, int8: the
+    kind of grid the surf-mask channel reads (its bake is the reference's)."""
+    gz = np.gradient(sdf, axis=0)
+    gy = np.gradient(sdf, axis=1)
+    gx = np.gradient(sdf, axis=2)
+    nrm = np.sqrt(gx * gx + gy * gy + gz * gz)
+    return np.where(nrm > 0, np.rint(np.abs(gz) / np.maximum(nrm, 1e-9) * 127), 0).astype(np.int8)
+
+
+def _variant(n, **extra):
+    w = synth.WORKLOADS["ramp_field"]
+    sc = w.scene()
+    ps = w.poses(sc, n)
+    kw = dict(width=w.width, height=w.height, range_units=w.range_units,
+              near_range=w.near_range, hit_eps=w.hit_eps, max_steps=w.max_steps)
+    keep = {}
+    ref = lockstep.render(sc.sdf, sc.mins, sc.cell, ps.origin, ps.yaw, ps.pitch, ps.ducked,
+                          keep=keep, **kw, **extra)
+    img, _ = oracle.render(sc.sdf, sc.mins, sc.cell, ps.origin, ps.yaw, ps.pitch, ps.ducked,
+                           threads=8, **kw, **extra)
+    return agreement.compare(sc.sdf, sc.mins, sc.cell, ps.origin, ps.yaw, ps.pitch, ps.ducked,
+                             img, ref, keep, list_max=None, **kw, **extra)
+
+
+def test_pinhole_agreement_with_the_reference_arithmetic():
+    """The pinhole camera through torch's CPU kernels (``_dirs_pinhole``,
+    vision.py:609-624: cos/sin of the view, the tangent-plane sum, rsqrt)
+    against the oracle's correctly rounded directions, 256 ramp_field envs:
+    the same bar, every outlier explained."""
+    a = _variant(256, pinhole=True)
+    assert a["within_tol"] >= 0.999 and a["exact"] >= 0.999, a
+    assert a["renderer_differs"] == 0 and a["ref_retrace_differs"] == 0, a
+    assert a["outliers_other"] == 0 and a["outliers"] == len(a["listed"]), a
+
+
+def test_surf_channel_agreement_with_the_reference_arithmetic():
+    """The surf-mask channel (the |n_z| code of the voxel under the clamped
+    depth over 127, vision.py:658-666) against the lockstep's: on 256
+    ramp_field envs with a gradient-derived |n_z| grid every channel value
+    whose depth agrees is equal, and the depth channel meets the bar. A
+    reference that divided by 128 (a planted slip) differs on most rays with
+    a nonzero code, none of them explained by a voxel-face tie."""
+    w = synth.WORKLOADS["ramp_field"]
+    snz = _nz_code_grid(w.scene().sdf)
+    a = _variant(256, surf_nz=snz)
+    assert a["within_tol"] >= 0.999, a
+    assert a["renderer_differs"] == 0 and a["ref_retrace_differs"] == 0, a
+    assert a["surf_other"] == 0 and a["outliers_other"] == 0, a
+    assert a["surf_differs"] == a["surf_with_depth_outlier"] + a["surf_tie"], a
+    # the planted slip: the lockstep's channel scaled by 127/128
+    sc = w.scene()
+    ps = w.poses(sc, 4)
+    kw = dict(width=w.width, height=w.height, range_units=w.range_units,
+              near_range=w.near_range, hit_eps=w.hit_eps, max_steps=w.max_steps)
+    keep = {}
+    ref = lockstep.render(sc.sdf, sc.mins, sc.cell, ps.origin, ps.yaw, ps.pitch, ps.ducked,
+                          keep=keep, surf_nz=snz, **kw)
+    ref[..., 1] = (ref[..., 1] * np.float32(127.0) / np.float32(128.0)).astype(np.float32)
+    img, _ = oracle.render(sc.sdf, sc.mins, sc.cell, ps.origin, ps.yaw, ps.pitch, ps.ducked,
+                           surf_nz=snz, threads=8, **kw)
+    b = agreement.compare(sc.sdf, sc.mins, sc.cell, ps.origin, ps.yaw, ps.pitch, ps.ducked,
+                          img, ref, keep, surf_nz=snz, **kw)
+    nonzero = int((img[..., 1] != 0).sum())
+    assert b["surf_differs"] > 0.9 * nonzero and b["surf_other"] > 0.9 * nonzero, b
+
+
+def test_lockstep_variants_agree_with_the_per_ray_oracle():
+    """The lockstep's pinhole and surf-mask renders against the oracle's on
+    small_ramps: bit-identical on at least 99.9% of rays."""
+    w = synth.WORKLOADS["small_ramps"]
+    sc = w.scene()
+    ps = w.poses(sc, 16)
+    kw = dict(width=w.width, height=w.height, range_units=w.range_units,
+              near_range=w.near_range, hit_eps=w.hit_eps, max_steps=w.max_steps)
+    for extra in (dict(pinhole=True), dict(surf_nz=_nz_code_grid(sc.sdf))):
+        a = lockstep.render(sc.sdf, sc.mins, sc.cell, ps.origin, ps.yaw, ps.pitch, ps.ducked,
+                            **kw, **extra)
+        b, _ = oracle.render(sc.sdf, sc.mins, sc.cell, ps.origin, ps.yaw, ps.pitch, ps.ducked,
+                             threads=8, **kw, **extra)
+        assert a.shape == b.shape
+        assert float((a == b).mean()) >= 0.999, extra.keys()
