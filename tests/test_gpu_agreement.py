@@ -9,7 +9,8 @@ and 1e-3 of its encoding, every ray outside it classified by
 oracle/agreement.py, and every outlier's GPU value reproduced by the
 oracle's march. None may be unexplained (class "other": two marches that part
 away from a voxel face); this host's torch build decides how many last-bit
-differences there are, so the other classes are counted, not fixed.
+differences there are, so the other classes are counted, not fixed. The
+same holds for the pinhole camera and for the surf-mask channel.
 """
 from __future__ import annotations
 
