@@ -358,10 +358,11 @@ def bench_goal(args, dev):
            "reference_torch_gpu": None, "cpu_baseline": None}
     if not args.no_ref and w.occ.size <= 64 * 1024 * 1024:
         _log("[bench] the reference's torch sweep loop on this GPU ...")
+        _reference_goal_loop_seconds(occ_dev, w.cell, lo, hi)     # first-call costs
         sweeps, sec = _reference_goal_loop_seconds(occ_dev, w.cell, lo, hi)
         res["reference_torch_gpu"] = {"value": round(sec * 1e3, 1), "unit": "ms", "sweeps": sweeps,
                                       "sample": "goalfield.py:232-270 loop as torch ops on "
-                                                "this GPU, one run"}
+                                                "this GPU, one run after a warm-up run"}
     if not args.no_cpu and w.occ.size <= 64 * 1024 * 1024:
         from oracle import goal as ogoal
         t0 = time.perf_counter()
