@@ -43,8 +43,6 @@ encoding's resolution (below 0.01 u for t <= 6144 at near 2000).
 """
 from __future__ import annotations
 
-import ctypes
-
 import numpy as np
 
 from . import _load, _ptr
