@@ -435,3 +435,45 @@ def test_surf_channel_reads_the_stop_voxel_of_each_ray():
                 assert img[e, r, c, 1] == F32(snz[iz, iy, ix]) / F32(127.0), (e, r, c, tr["why"])
     assert hits > 50
     assert slips > 0.5 * hits
+
+
+def test_the_sample_by_sample_trace_reproduces_the_render():
+    """oracle_march_trace (the per-sample record the agreement classifier
+    re-traces rays with) marches exactly as the render does: for 300 random
+    rays of small_ramps its final depth encodes to the render's value, its
+    sample count is the render's load count, its first sample is the eye's
+    voxel, each recorded t is the previous one plus max(0.9 s, min_step),
+    and the stop reason matches the last sample."""
+    from oracle import agreement
+    from surfgym import synth
+    w = synth.WORKLOADS["small_ramps"]
+    sc = w.scene()
+    ps = w.poses(sc, 6)
+    kw = dict(width=w.width, height=w.height, range_units=w.range_units,
+              near_range=w.near_range, hit_eps=w.hit_eps, max_steps=w.max_steps)
+    img, loads = oracle.render(sc.sdf, sc.mins, sc.cell, ps.origin, ps.yaw, ps.pitch, ps.ducked,
+                               **kw)
+    lib = oracle._load()
+    rng = np.random.default_rng(3)
+    mstep = F32(0.3 * sc.cell)
+    for _ in range(300):
+        e, r, c = int(rng.integers(6)), int(rng.integers(w.height)), int(rng.integers(w.width))
+        eye = (F32(ps.origin[e, 0]), F32(ps.origin[e, 1]),
+               F32(F32(ps.origin[e, 2]) + F32(12.0 if ps.ducked[e] else 17.0)))
+        d = agreement._dir(lib, w.width, w.height, 120.0, 90.0, ps.yaw[e], ps.pitch[e], r, c)
+        tr = agreement.trace(sc.sdf, sc.mins, sc.cell, eye, d, range_units=w.range_units,
+                             hit_eps=w.hit_eps, min_step=float(mstep), max_steps=w.max_steps)
+        t = min(F32(tr["t"]), F32(w.range_units))
+        assert F32(oracle.encode(float(t), w.near_range)) == img[e, r, c]
+        assert len(tr["t_k"]) == loads[e, r, c]
+        assert tr["t_k"][0] == 0.0
+        for k in range(1, len(tr["t_k"])):
+            step = max(F32(tr["s_k"][k - 1] * F32(0.9)), mstep)
+            assert tr["t_k"][k] == F32(tr["t_k"][k - 1] + step)
+        last = tr["s_k"][-1]
+        if tr["why"] == "hit":
+            assert not last > w.hit_eps
+        elif tr["why"] == "range":
+            assert last > w.hit_eps and not tr["t_k"][-1] < w.range_units
+        else:
+            assert len(tr["t_k"]) == w.max_steps
