@@ -25,7 +25,14 @@ ramp_field_f16_bf16 ramp_field scene stored f16,  8192     96      6144 / 2000
                     bf16 output
 ramp_field_r16_bf16 ramp_field scene stored as    8192     96      6144 / 2000
                     r16 bricks, bf16 output
+map_scale           1536x1536x280 @32 u stored    2048     64      11500 / 2000
+                    f16, track of 600 segments
 =================== ============================ ======== ======= ===========
+
+map_scale is no benchmark configuration: it is a map of the size the
+reference's production map has (surf_src_cannonball, ~654 M voxels at 32 u,
+fp16; python/surfgym/vision.py:433-437) with the reference's production
+sensor (range 11500, near 2000, 64 steps; docs/perf-results.md:73).
 
 hit_eps is 1 u in every workload. Scene seeds are 1000+k and pose seeds
 2000+k (numpy PCG64) for the k-th row above; the two fused-output rows share
@@ -324,6 +331,10 @@ def _sparse_scene():
     return ramp_scene(256, 256, 128, 16.0, 16, 0, 1003)
 
 
+def _map_scale_scene():
+    return track_scene(1536, 1536, 280, 32.0, 600, 1006)
+
+
 SMALL_DIAG = float(np.linalg.norm(np.array([64, 64, 32]) * 16.0))       # 1536
 TRACK_DIAG = float(np.linalg.norm(np.array([1024, 1024, 256]) * 16.0))  # 4096*sqrt(33)
 
@@ -349,6 +360,9 @@ WORKLOADS = {
         "ramp_field_r16_bf16", _field_scene, lambda s, n: poses_above_ramps(s, n, 2004),
         n_envs=8192, max_steps=96, range_units=6144.0, near_range=2000.0,
         store="r16", out_dtype="bf16"),
+    "map_scale": Workload(
+        "map_scale", _map_scale_scene, lambda s, n: poses_above_ramps(s, n, 2006),
+        n_envs=2048, max_steps=64, range_units=11500.0, near_range=2000.0, store="f16"),
 }
 
 

@@ -9,7 +9,9 @@ voxels, python/surfgym/vision.py:433-437, 2.6 GB as fp32). This renders a
 that the samples near the top of the grid and every ray that leaves through
 the top (clamped to the last layer, vision.py:104-106) read bricks past the
 2 GiB offset, and compares the image with the oracle's bit for bit, with
-the border voxels read from the bricks and from the face copies.
+the border voxels read from the bricks and from the face copies. A map of
+the reference's production size, stored fp16 as the reference stores it,
+renders exactly as well.
 """
 from __future__ import annotations
 
@@ -55,3 +57,24 @@ def test_a_grid_above_2_gib_renders_equal_to_the_oracle(dev):
     z_end = eye_z[:, None, None] + d[..., 2] * t
     iz = np.clip(np.floor((z_end - sc.mins[2]) / CELL), 0, NZ - 1)
     assert (iz >= 512).mean() > 0.2, (iz >= 512).mean()
+
+
+def test_a_map_of_the_references_production_size_renders_exactly(dev):
+    """map_scale: 661 M voxels at 32 u (the size of the reference's
+    production map, vision.py:433-437) with its production sensor (range
+    11500, near 2000, 64 steps), in the reference's fp16 store: 16 envs
+    equal the oracle's render of the fp16-rounded grid bit for bit."""
+    store = "f16"
+    w = synth.WORKLOADS["map_scale"]
+    sc = w.scene()
+    ps = w.poses(sc, 16)
+    kw = dict(width=w.width, height=w.height, range_units=w.range_units,
+              near_range=w.near_range, max_steps=w.max_steps, hit_eps=w.hit_eps)
+    print(f"case map_scale {sc.nx}x{sc.ny}x{sc.nz} {store}, 16 envs", flush=True)
+    lid = vision.GpuLidar.from_grid(sc.sdf, sc.mins, sc.cell, device=dev,
+                                    grid_dtype=torch.float16, **kw)
+    want, _ = oracle.render(sc.sdf, sc.mins, sc.cell, ps.origin, ps.yaw, ps.pitch, ps.ducked,
+                            store=store, threads=16, **kw)
+    got = lid.render(*[torch.as_tensor(v, device=dev)
+                       for v in (ps.origin, ps.yaw, ps.pitch, ps.ducked)]).cpu().numpy()
+    assert np.array_equal(got, want), int((got != want).sum())
