@@ -1,16 +1,18 @@
-"""GPU render against the reference's own CPU arithmetic at the headline size.
+"""GPU render against the reference's own CPU arithmetic at full size.
 
 The reference's CPU render (python/surfgym/vision.py:596-657) takes cos/sin/
 exp from torch's CPU kernels; oracle/lockstep.py restates it with those same
-calls. This renders all 2048 ramp_field envs (16.8 M rays) on the GPU, the
-same poses through the lockstep on this host's cores, and holds the pair to
-the accuracy bar: >= 99.9% of rays within 0.5 u of the reference's depth
-and 1e-3 of its encoding, every ray outside it classified by
-oracle/agreement.py, and every outlier's GPU value reproduced by the
-oracle's march. None may be unexplained (class "other": two marches that part
-away from a voxel face); this host's torch build decides how many last-bit
-differences there are, so the other classes are counted, not fixed. The
-same holds for the pinhole camera and for the surf-mask channel.
+calls. This renders every env of a workload on the GPU (ramp_field, the
+headline: 2048 envs, 16.8 M rays; winding_track: 2048 envs over the 1 GiB
+grid; sparse_grazing: 8192 envs, 67 M rays), the same poses through the
+lockstep on this host's cores, and holds the pair to the accuracy bar:
+>= 99.9% of rays within 0.5 u of the reference's depth and 1e-3 of its
+encoding, every ray outside it classified by oracle/agreement.py, and every
+outlier's GPU value reproduced by the oracle's march. None may be
+unexplained (class "other": two marches that part away from a voxel face);
+this host's torch build decides how many last-bit differences there are, so
+the other classes are counted, not fixed. The same holds for the pinhole
+camera and for the surf-mask channel.
 """
 from __future__ import annotations
 
@@ -34,6 +36,48 @@ def _nz_code_grid(sdf):
     return np.where(nrm > 0, np.rint(np.abs(gz) / np.maximum(nrm, 1e-9) * 127), 0).astype(np.int8)
 
 
+def _agreement(dev, name, variant=None):
+    """Render workload `name` on the GPU and through the lockstep; return
+    the agreement record and the GPU image."""
+    w = synth.WORKLOADS[name]
+    sc = w.scene()
+    ps = w.poses(sc)
+    extra = {}
+    if variant == "pinhole":
+        extra = dict(pinhole=True)
+    elif variant == "surf_mask":
+        extra = dict(surf_nz=_nz_code_grid(sc.sdf))
+    print(f"case agreement {w.name} {variant or 'equiangular'}: {len(ps)} envs", flush=True)
+    lid = vision.GpuLidar.from_grid(sc.sdf, sc.mins, sc.cell, width=w.width, height=w.height,
+                                    range_units=w.range_units, near_range=w.near_range,
+                                    max_steps=w.max_steps, hit_eps=w.hit_eps,
+                                    grid_dtype=torch.float32, device=dev, **extra)
+    img = lid.render(torch.as_tensor(ps.origin, device=dev), torch.as_tensor(ps.yaw, device=dev),
+                     torch.as_tensor(ps.pitch, device=dev),
+                     torch.as_tensor(ps.ducked, device=dev)).cpu().numpy()
+    del lid
+    kw = dict(width=w.width, height=w.height, range_units=w.range_units,
+              near_range=w.near_range, hit_eps=w.hit_eps, max_steps=w.max_steps)
+    torch.set_num_threads(max(1, min(16, len(os.sched_getaffinity(0)))))
+    keep = {}
+    ref = lockstep.render(sc.sdf, sc.mins, sc.cell, ps.origin, ps.yaw, ps.pitch, ps.ducked,
+                          keep=keep, **kw, **extra)
+    print(f"lockstep render done ({ref.size} values)", flush=True)
+    a = agreement.compare(sc.sdf, sc.mins, sc.cell, ps.origin, ps.yaw, ps.pitch, ps.ducked,
+                          img, ref, keep, list_max=None, **kw, **extra)
+    print({k: v for k, v in a.items() if k != "listed"}, flush=True)
+    assert a["rays"] == w.rays
+    return a, img
+
+
+def _assert_bar(a):
+    assert a["within_tol"] >= 0.999 and a["exact"] >= 0.999, a
+    assert a["renderer_differs"] == 0 and a["ref_retrace_differs"] == 0
+    assert a["outliers_other"] == 0, [o for o in a["listed"] if o["class"] == "other"]
+    assert a["outliers"] == len(a["listed"]) == (a["outliers_grazing"] + a["outliers_step_phase"]
+                                                 + a["outliers_tie_other"])
+
+
 @pytest.mark.parametrize("variant", ["pinhole", "surf_mask"])
 def test_variant_renders_meet_the_bar_against_the_reference_arithmetic(dev, variant):
     """The pinhole camera and the surf-mask channel at the headline size:
@@ -42,60 +86,25 @@ def test_variant_renders_meet_the_bar_against_the_reference_arithmetic(dev, vari
     clamped depth over 127), every depth outlier classified, and every |n_z|
     that differs where the depths agree explained by a voxel-face tie at the
     march's end point."""
-    w = synth.WORKLOADS["ramp_field"]
-    sc = w.scene()
-    ps = w.poses(sc)
-    extra = dict(pinhole=True) if variant == "pinhole" else dict(surf_nz=_nz_code_grid(sc.sdf))
-    print(f"case agreement {w.name} {variant}: {len(ps)} envs", flush=True)
-    lid = vision.GpuLidar.from_grid(sc.sdf, sc.mins, sc.cell, width=w.width, height=w.height,
-                                    range_units=w.range_units, near_range=w.near_range,
-                                    max_steps=w.max_steps, hit_eps=w.hit_eps,
-                                    grid_dtype=torch.float32, device=dev, **extra)
-    img = lid.render(torch.as_tensor(ps.origin, device=dev), torch.as_tensor(ps.yaw, device=dev),
-                     torch.as_tensor(ps.pitch, device=dev),
-                     torch.as_tensor(ps.ducked, device=dev)).cpu().numpy()
-    kw = dict(width=w.width, height=w.height, range_units=w.range_units,
-              near_range=w.near_range, hit_eps=w.hit_eps, max_steps=w.max_steps)
-    torch.set_num_threads(max(1, min(16, len(os.sched_getaffinity(0)))))
-    keep = {}
-    ref = lockstep.render(sc.sdf, sc.mins, sc.cell, ps.origin, ps.yaw, ps.pitch, ps.ducked,
-                          keep=keep, **kw, **extra)
-    a = agreement.compare(sc.sdf, sc.mins, sc.cell, ps.origin, ps.yaw, ps.pitch, ps.ducked,
-                          img, ref, keep, list_max=None, **kw, **extra)
-    print({k: v for k, v in a.items() if k != "listed"}, flush=True)
-    assert a["within_tol"] >= 0.999 and a["exact"] >= 0.999, a
-    assert a["renderer_differs"] == 0 and a["ref_retrace_differs"] == 0
-    assert a["outliers_other"] == 0, [o for o in a["listed"] if o["class"] == "other"]
+    a, _ = _agreement(dev, "ramp_field", variant)
+    _assert_bar(a)
     if variant == "surf_mask":
         assert a["surf_other"] == 0, a
         assert a["surf_differs"] == a["surf_with_depth_outlier"] + a["surf_tie"]
 
 
 def test_headline_render_meets_the_bar_against_the_reference_arithmetic(dev):
-    w = synth.WORKLOADS["ramp_field"]
-    sc = w.scene()
-    ps = w.poses(sc)
-    print(f"case agreement {w.name}: {len(ps)} envs", flush=True)
-    lid = vision.GpuLidar.from_grid(sc.sdf, sc.mins, sc.cell, width=w.width, height=w.height,
-                                    range_units=w.range_units, near_range=w.near_range,
-                                    max_steps=w.max_steps, hit_eps=w.hit_eps,
-                                    grid_dtype=torch.float32, device=dev)
-    img = lid.render(torch.as_tensor(ps.origin, device=dev), torch.as_tensor(ps.yaw, device=dev),
-                     torch.as_tensor(ps.pitch, device=dev),
-                     torch.as_tensor(ps.ducked, device=dev)).cpu().numpy()
-    kw = dict(width=w.width, height=w.height, range_units=w.range_units,
-              near_range=w.near_range, hit_eps=w.hit_eps, max_steps=w.max_steps)
-    torch.set_num_threads(max(1, min(16, len(os.sched_getaffinity(0)))))
-    keep = {}
-    ref = lockstep.render(sc.sdf, sc.mins, sc.cell, ps.origin, ps.yaw, ps.pitch, ps.ducked,
-                          keep=keep, **kw)
-    a = agreement.compare(sc.sdf, sc.mins, sc.cell, ps.origin, ps.yaw, ps.pitch, ps.ducked,
-                          img, ref, keep, list_max=None, **kw)
-    print({k: v for k, v in a.items() if k != "listed"}, flush=True)
+    a, img = _agreement(dev, "ramp_field")
     assert a["rays"] == 2048 * 64 * 128
-    assert a["within_tol"] >= 0.999 and a["exact"] >= 0.999, a
-    assert a["renderer_differs"] == 0 and a["ref_retrace_differs"] == 0
-    assert a["outliers_other"] == 0, [o for o in a["listed"] if o["class"] == "other"]
-    assert a["outliers"] == len(a["listed"]) == (a["outliers_grazing"] + a["outliers_step_phase"]
-                                                 + a["outliers_tie_other"])
+    _assert_bar(a)
     assert np.isfinite(img).all()
+
+
+@pytest.mark.parametrize("name", ["winding_track", "sparse_grazing"])
+def test_the_other_full_size_workloads_meet_the_bar(dev, name):
+    """The 1 GiB track grid (long rays over open ground, 96 steps) and the
+    sparse scene whose rays graze the ground at 8192 envs, against the
+    lockstep render at their full sizes."""
+    a, _ = _agreement(dev, name)
+    _assert_bar(a)
+    print([o for o in a["listed"] if o["class"] == "tie_other"], flush=True)
